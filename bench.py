@@ -1,0 +1,266 @@
+"""Benchmark of the quantized-weight products on one MI355X.
+
+Headline (BASELINE.json metric): int4 GEMM HBM GB/s at M=1 on the 27B-scale decode layer set:
+(K, N) = (5120, 17408) x 2, (17408, 5120), (5120, 6144), (6144, 5120) symmetric int4 group 128, plus the int4
+output head K=5120, N=248320 (argmax epilogue). A step is one pass over FOUR distinct device copies of the layer set
+(680 MB, beyond the 256 MB MALL) and the head, captured once in a HIP graph and replayed; value = algorithmic bytes
+of the step / step time. Extra lines: the same at M=5, the prefill GEMM at M=2048 in TFLOP/s, W8A16 at M=1.
+
+Algorithmic bytes per product: int4 K N / 2 + (K / 128) N 2 [+ (K / 128) N / 2 zero points] + M K 2 + M N 2;
+int8 K N + 2 N + 2 M K + 2 M N. Flops 2 M N K.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8000.0  # GB/s, MI355X
+BF16_PEAK = 2500.0  # TFLOP/s dense, MI355X
+
+SET_27B = [(5120, 17408), (5120, 17408), (17408, 5120), (5120, 6144), (6144, 5120)]
+HEAD_27B = (5120, 248320)
+
+
+def int4_bytes(k, n, m, zp=False):
+    return k * n // 2 + (k // 128) * n * 2 + ((k // 128) * n // 2 if zp else 0) + m * k * 2 + m * n * 2
+
+
+def int8_bytes(k, n, m):
+    return k * n + 2 * n + 2 * m * k + 2 * m * n
+
+
+def quant(seed, kind, k, n):
+    from tests.helpers import make_quant
+
+    return make_quant(seed, kind, n, k)
+
+
+def upload_copies(gemm, q, copies):
+    """`copies` distinct device matrices of the same packed data."""
+    from qwenny_amd._lib import check, lib
+    from qwenny_amd.core import Mat, P, Wt, pack_quant
+    import ctypes
+
+    z = q.zero_points()
+    wt = Wt.I8 if q.bits == 8 else (Wt.I4 if (z == 8).all() else Wt.I4Z)
+    order = np.arange(q.rows)
+    codes, scales, zs = pack_quant(q, order, wt, None if wt != Wt.I4Z else z)
+    mats = []
+    for _ in range(copies):
+        h = P()
+        check(lib().qh_mat_upload(gemm._ctx, int(wt), q.rows, q.cols, codes.ctypes.data, scales.ctypes.data,
+                                  None if zs is None else zs.ctypes.data, q.rows, ctypes.byref(h)))
+        mats.append(Mat(gemm, h))
+    return mats
+
+
+class Step:
+    """A list of product launches (mat, m, epi, bytes, flops) with their buffers, replayable as a HIP graph."""
+
+    def __init__(self, gemm, m, kmax):
+        import torch
+
+        self.gemm, self.m = gemm, m
+        self.launches = []
+        self.x = torch.randn(max(m, 1), kmax, device="cuda").to(torch.bfloat16)
+        self.keys = torch.zeros(max(m, 64), dtype=torch.int64, device="cuda")
+        self.ys = {}
+
+    def add(self, mat, epi, nbytes, flops):
+        import torch
+
+        from qwenny_amd import Epi
+
+        rows = mat.rows
+        split = mat.split(self.m) if epi == Epi.Plain and self.m <= 16 else 1
+        key = (rows, split, epi)
+        if key not in self.ys:
+            self.ys[key] = torch.empty(split * self.m * rows, dtype=torch.float32, device="cuda")
+        self.launches.append((mat, epi, self.ys[key], nbytes, flops))
+
+    def run(self, stream=None):
+        from qwenny_amd import Epi
+
+        for mat, epi, y, _, _ in self.launches:
+            if epi == Epi.Argmax:
+                self.gemm.run(stream, self.m, mat, self.x, y, epi, n_out=self.m, keys=self.keys)
+            else:
+                self.gemm.run(stream, self.m, mat, self.x, y, epi)
+
+    def bytes(self):
+        return sum(b for *_, b, _ in self.launches)
+
+    def flops(self):
+        return sum(f for *_, f in self.launches)
+
+
+def time_step(step, steps, warmup, graph=True):
+    """ms per step over `steps` replays, HIP events on the launching stream, after `warmup` replays."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    g = None
+    if graph:
+        step.run()  # the kernels' first launches outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                step.run(s)
+        torch.cuda.synchronize()
+    go = g.replay if g is not None else step.run
+    for _ in range(warmup):
+        go()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        go()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's CPU form (Quant::row_into to f32 then an f32 dot, threaded over rows) on the host cores, on a
+    bounded sample of the headline workload: whole passes over the 27B layer set at M=1 until `budget_s` is spent."""
+    import oracle
+    from qwenny_amd.synth import activations
+
+    threads = min(os.cpu_count() or 1, 16)
+    qs = [quant(100 + i, "i4", k, n) for i, (k, n) in enumerate(SET_27B)]
+    xs = {k: activations(9, "x", 1, k) for k, _ in SET_27B}
+    done_bytes, t0, passes = 0, time.perf_counter(), 0
+    while True:
+        for q, (k, n) in zip(qs, SET_27B):
+            oracle.gemm_f32(4, 128, q.q, q.scales, q.offsets, xs[k], threads=threads)
+            done_bytes += int4_bytes(k, n, 1)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} pass(es) over the 27B decode layer set (5 matrices, 170.5 MB) at M=1, "
+                      f"scalar C restatement of Quant::row_into + f32 dot, {threads} threads, {el:.1f} s"}
+
+
+def load_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if there is one for this workload."""
+    p = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "single-GPU build: the products run on one MI355X; --gpus must be 1 "
+                                   "(how they would shard is described in DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+
+    from qwenny_amd import Epi, Gemm
+
+    torch.cuda.init()
+    gemm = Gemm.load(0)
+    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8"}
+    print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
+    set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
+    head = upload_copies(gemm, quant(200, "i4", *HEAD_27B), 1)[0]
+
+    def decode_step(m):
+        st = Step(gemm, m, 17408)
+        for c in range(4):
+            for mats, (k, n) in zip(set_mats, SET_27B):
+                st.add(mats[c], Epi.Plain, int4_bytes(k, n, m), 2 * m * k * n)
+        st.add(head, Epi.Argmax, int4_bytes(*HEAD_27B, m), 2 * m * HEAD_27B[0] * HEAD_27B[1])
+        return st
+
+    out = {}
+    step = decode_step(1)
+    ms = time_step(step, args.steps, args.warmup, not args.no_graph)
+    gbs = step.bytes() / (ms * 1e-3) / 1e9
+    launches = len(step.launches)
+    out["m1"] = {"ms_per_step": ms, "GB/s": gbs, "launches": launches, "bytes": step.bytes()}
+    print(f"# M=1 27B set x4 + head: {ms:.4f} ms/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK:.1%} of 8 TB/s)",
+          file=sys.stderr, flush=True)
+
+    extra = {}
+    if "m5" in only:
+        st5 = decode_step(5)
+        ms5 = time_step(st5, args.steps, args.warmup, not args.no_graph)
+        extra["m5_GBps"] = round(st5.bytes() / (ms5 * 1e-3) / 1e9, 1)
+        print(f"# M=5: {ms5:.4f} ms/step, {extra['m5_GBps']} GB/s", file=sys.stderr, flush=True)
+    if "prefill" in only:
+        pf = {}
+        for i, (k, n) in enumerate([(5120, 17408), (17408, 5120), (5120, 6144)]):
+            mat = set_mats[[0, 2, 3][i]][0]
+            st = Step(gemm, 2048, k)
+            st.add(mat, Epi.Plain, int4_bytes(k, n, 2048), 2 * 2048 * k * n)
+            msp = time_step(st, max(10, args.steps // 10), 3, False)
+            tf = st.flops() / (msp * 1e-3) / 1e12
+            pf[f"{k}x{n}"] = round(tf, 1)
+            print(f"# prefill M=2048 K={k} N={n}: {msp:.3f} ms, {tf:.1f} TFLOP/s ({tf / BF16_PEAK:.1%})",
+                  file=sys.stderr, flush=True)
+        extra["prefill_m2048_TFLOPs"] = pf
+    if "int8" in only:
+        i8 = [upload_copies(gemm, quant(300 + i, "i8", k, n), 4) for i, (k, n) in
+              enumerate([(5120, 17408), (17408, 5120)])]
+        st = Step(gemm, 1, 17408)
+        for c in range(4):
+            for mats, (k, n) in zip(i8, [(5120, 17408), (17408, 5120)]):
+                st.add(mats[c], Epi.Plain, int8_bytes(k, n, 1), 2 * k * n)
+        ms8 = time_step(st, args.steps, args.warmup, not args.no_graph)
+        extra["int8_m1_GBps"] = round(st.bytes() / (ms8 * 1e-3) / 1e9, 1)
+        print(f"# int8 M=1: {ms8:.4f} ms/step, {extra['int8_m1_GBps']} GB/s", file=sys.stderr, flush=True)
+
+    per_launch_bytes = step.bytes() / launches
+    per_launch_s = ms * 1e-3 / launches
+    line = {
+        "metric": "int4 GEMM HBM GB/s (% of 8 TB/s) at M=1/5; TFLOP/s (% bf16 MFMA peak) at M=2048",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded int4 codes, bf16 scales U(0.002,0.02), bf16 x N(0,1))",
+        "config": {"workload": "27B-scale int4 sym g128 decode M=1: (5120,17408)x2,(17408,5120),(5120,6144),"
+                               "(6144,5120) x4 device copies + head (5120,248320) argmax",
+                   "m": 1, "copies": 4, "graph": not args.no_graph},
+        "roofline": {"bound": "hbm", "achieved": round(per_launch_bytes / per_launch_s / 1e9, 1), "peak": HBM_PEAK,
+                     "unit": "GB/s", "frac": round(per_launch_bytes / per_launch_s / 1e9 / HBM_PEAK, 4),
+                     "traffic": load_traffic("skinny_i4_m1_27b"),
+                     "kernel": "skinny_kernel (int4, M=1)", "bytes_per_launch": round(per_launch_bytes),
+                     "launches_per_step": launches},
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,180 @@
+/*
+ * qwenny_hip.h — C ABI of the MI355X (gfx950) quantized-weight matrix products.
+ *
+ * This is the boundary that replaces qwenny's CUDA product runtime (`src/cuda/core.rs`) behind the same Rust call
+ * sites (`Stack::gemm`, `Mat::stack`, `Mat::marlin_rows`, `Gemm::put_block`). Every entry point takes plain pointers
+ * and sizes; device pointers are opaque `void*` (HIP device memory), streams are `hipStream_t` passed as `void*`.
+ * No C++ exception crosses this boundary: functions return an int status (>= 0 success, < 0 error) and
+ * `qh_last_error()` describes the last failure of the calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   Quant (checkpoint.rs:21-31), Quant::row_into (:39-47), Quant::zero_points (:72-82), Quant::stack (:85-99),
+ *   Checkpoint::packed_matrix (:408-453), row_order (cuda/core.rs:108-114), Mat (:94-104),
+ *   Mat::new / pack (:127-135, :338-389), Mat::marlin_rows (:140-153), Mat::marlin (:159-164), Mat::int8 (:168-191),
+ *   part_len (:315-318), Gemm::load (:436-481), Gemm::run / run_split (:485-561), Gemm::put_block (:619-657),
+ *   Gemm::block_stage (:675-680).
+ */
+#ifndef QWENNY_HIP_H
+#define QWENNY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (negative = error). */
+#define QH_OK 0
+#define QH_EINVAL -1   /* bad argument or shape the layout does not take */
+#define QH_EHIP -2     /* a HIP runtime call failed */
+#define QH_ENOMEM -3   /* device or host allocation failed */
+#define QH_ENOTFIT -4  /* the matrix does not fit this storage (e.g. non-integer zero points) */
+
+/* How a matrix is stored for the kernels (core.rs:65-79 `Wt`, without F16: dense 16-bit products are not built). */
+enum qh_wt {
+    QH_WT_I8 = 1,  /* int8 stored q + 128, an f32 scale per row and 128 columns (core.rs Wt::I8) */
+    QH_WT_I4 = 2,  /* symmetric int4 (zero point 8), bf16 scale per row and 128 columns (core.rs Wt::Marlin) */
+    QH_WT_I4Z = 3, /* int4 with a 4-bit zero point per row and 128 columns (core.rs Wt::MarlinZ) */
+    QH_WT_I4_S32 = 4, /* QH_WT_I4 with f32 scales: scales that bf16 does not hold exactly (f16 / f32 checkpoints) */
+    QH_WT_I4Z_S32 = 5 /* QH_WT_I4Z with f32 scales */
+};
+
+/* Epilogue of a product (core.rs:52-58 `Epi`). */
+enum qh_epi {
+    QH_EPI_PLAIN = 0,  /* f32 y[split][n][rows], split-K partials the consumer sums */
+    QH_EPI_SILU = 1,   /* bf16 y[n][rows/2] = silu(gate) * up over row_order's interleaved tiles */
+    QH_EPI_ARGMAX = 2  /* f32 logits y[n_out][rows] and the running argmax key per logit row in keys[] */
+};
+
+/* A quantized matrix [rows][cols] as stored (checkpoint.rs:21-31 `Quant`): w = q * scale + offset per group of a
+ * row. q: [rows][cols * bits / 32] words, value c of a row in word c * bits / 32 at bit (c % (32 / bits)) * bits.
+ * scales, offsets: [rows][cols / group] f32. */
+typedef struct qh_quant {
+    int32_t bits;
+    int32_t group;
+    size_t rows;
+    size_t cols;
+    const uint32_t* q;
+    const float* scales;
+    const float* offsets;
+} qh_quant;
+
+typedef struct qh_ctx qh_ctx;
+typedef struct qh_mat qh_mat;
+
+/* Read-only description of a device matrix (core.rs:94-104 `Mat`). */
+typedef struct qh_mat_desc {
+    int32_t wt;         /* enum qh_wt */
+    size_t rows;        /* packed rows (outputs), a multiple of 16 */
+    size_t cols;        /* columns (K), a multiple of 128 */
+    size_t valid;       /* rows that count for the argmax (core.rs Mat::valid) */
+    size_t code_bytes;  /* device bytes of the packed codes */
+    size_t scale_bytes; /* device bytes of the scales */
+    size_t zero_bytes;  /* device bytes of the zero points (0 unless QH_WT_I4Z) */
+} qh_mat_desc;
+
+/* The last error of the calling thread ("" if none). */
+const char* qh_last_error(void);
+
+/* ---- host-side weight formats (no GPU needed) ----------------------------------------------------------------- */
+
+/* Checkpoint::packed_matrix (checkpoint.rs:408-453): compressed-tensors pack-quantized tensors into Quant fields.
+ * packed: weight_packed [rows][words] int32; scale: weight_scale as f32 [rows * groups] (callers convert bf16/f16);
+ * zp: weight_zero_point words or NULL (symmetric: zero 2^(bits-1)); zp_rows/zp_cols its shape (packed along rows:
+ * [ceil(rows/per)][groups], or along groups: [rows][ceil(groups/per)]); cols: weight_shape[1] or 0 (from words);
+ * group: 0 = one group per row (strategy "channel"). Writes bits/group/cols to *out and scales/offsets to the
+ * caller's arrays [rows * groups]; out->q points at `packed`. */
+int qh_quant_from_packed(const uint32_t* packed, size_t rows, size_t words, size_t cols, int bits, int group,
+                         const float* scale, const uint32_t* zp, size_t zp_rows, size_t zp_cols, float* scales_out,
+                         float* offsets_out, qh_quant* out);
+
+/* Quant::zero_points (checkpoint.rs:72-82): z[rows * groups] if every offset is -z * scale for an integer z in
+ * [0, 2^bits - 1] (within 1e-3). Returns 1 if so, 0 if not (z unspecified), < 0 on error. */
+int qh_quant_zero_points(const qh_quant* q, uint8_t* z);
+
+/* Quant::row_into (checkpoint.rs:39-47): row r dequantized into out[cols] (f32). */
+int qh_quant_row_into(const qh_quant* q, size_t r, float* out);
+
+/* row_order (core.rs:108-114): packed row i <- original row out[i]. silu: gate/up interleaved per 16 rows. */
+int qh_row_order(size_t rows, int silu, size_t* out);
+
+/* Byte sizes of the gfx950 tile layout for a matrix of `rows` packed rows (padded up to 16) and `cols` columns. */
+int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_bytes, size_t* scale_bytes, size_t* zero_bytes);
+
+/* The load-time repacker: rows `order[0..n)` of `q` (a Quant of bits 4 or 8, group a multiple of 128 or a whole row)
+ * into the gfx950 tile layout (replaces pack_marlin, core.rs:245-311, and frags_int8, :223-242). wt QH_WT_I4 needs
+ * zero points 8 everywhere, QH_WT_I4Z takes `zeros` [rows * groups] (Quant::zero_points), QH_WT_I8 needs zero points
+ * 128; the _S32 storages keep f32 scales. codes / scales / zeros: buffers of qh_packed_sizes. Host-side,
+ * multithreaded. */
+int qh_pack_quant(const qh_quant* q, const uint8_t* zeros, const size_t* order, size_t n, int wt, void* codes,
+                  void* scales, void* zeros_out);
+
+/* The repacker's inverse for one packed row p: its stored values (int4 0..15 or int8 q + 128) into vals[cols], its
+ * per-128-column scales as f32 into sc[cols / 128] and zero points into z[cols / 128] (8 or 128 when symmetric). */
+int qh_unpack_row(int wt, size_t rows, size_t cols, const void* codes, const void* scales, const void* zeros,
+                  size_t p, uint8_t* vals, float* sc, uint8_t* z);
+
+/* Mat::new / pack int8 branch (core.rs:127-135, :338-389): dense bf16 [rows][cols] rows `order` requantized to
+ * symmetric int8 per row and 128 columns (scale max|w| / 127, 1 if 0; q = round half away from zero, clamped to
+ * +-127, stored + 128) into the QH_WT_I8 layout. */
+int qh_pack_dense_int8(const uint16_t* bf16, size_t rows, size_t cols, const size_t* order, size_t n, void* codes,
+                       void* scales);
+
+/* ---- device: context, matrices, products ---------------------------------------------------------------------- */
+
+/* Gemm::load (core.rs:436-481): a context on `device` (makes it current on this thread). */
+int qh_open(int device, qh_ctx** out);
+void qh_close(qh_ctx* ctx);
+
+/* Mat::upload (core.rs:117-124): a device matrix from packed host buffers (qh_pack_*); `valid` rows count. */
+int qh_mat_upload(qh_ctx* ctx, int wt, size_t rows, size_t cols, const void* codes, const void* scales,
+                  const void* zeros, size_t valid, qh_mat** out);
+
+/* Mat::marlin / Mat::int8 (core.rs:159-191): a stored int4 / int8 Quant, packed in row_order(silu) and uploaded.
+ * int4 gives QH_WT_I4 (all zero points 8) or QH_WT_I4Z, their _S32 forms when a scale is not exact in bf16; int8
+ * needs zero points 128. QH_ENOTFIT if it does not fit. */
+int qh_mat_quant(qh_ctx* ctx, const qh_quant* q, int silu, qh_mat** out);
+
+/* Mat::marlin_rows (core.rs:140-153): rows `rows[0..n)` (n a multiple of 16) of an int4 Quant with zero points
+ * `zeros`, in a matrix of `cap` rows (a multiple of 16); the rest are room for qh_put_block and not valid. */
+int qh_mat_quant_rows(qh_ctx* ctx, const qh_quant* q, const uint8_t* zeros, const size_t* rows, size_t n, size_t cap,
+                      qh_mat** out);
+
+/* Mat::new int8 (core.rs:127-135): dense bf16 [rows][cols] requantized to int8 (qh_pack_dense_int8), uploaded. */
+int qh_mat_dense_int8(qh_ctx* ctx, const uint16_t* bf16, size_t rows, size_t cols, int silu, qh_mat** out);
+
+void qh_mat_free(qh_mat* m);
+int qh_mat_describe(const qh_mat* m, qh_mat_desc* out);
+
+/* Copy a device matrix's packed buffers back to the host (sizes from qh_mat_describe); zeros may be NULL. */
+int qh_mat_download(const qh_mat* m, void* codes, void* scales, void* zeros);
+
+/* Split-K factor a plain product of n tokens uses on m (core.rs Mat::split). */
+int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n);
+
+/* part_len (core.rs:315-318): floats the plain products of `mats` write at most, for up to `max_tok` tokens. */
+size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok);
+
+/* Gemm::run_split (core.rs:485-561): y = w . x on `stream`.
+ *   x: bf16 [.][ldx] device (ldx = 0: cols); n tokens (rows of x);
+ *   epi QH_EPI_PLAIN: y f32 [split][n][rows], returns split (1 when `whole`);
+ *   epi QH_EPI_SILU: y bf16 [n][rows / 2];
+ *   epi QH_EPI_ARGMAX: logit rows: token t reads x row out_rows[t] (int32 device, NULL: t) for t < n_out; y f32
+ *     [n_out][rows]; keys[t] (u64 device, cleared by the caller) = max(keys[t], (ordered(v) << 32) | ~o) over the
+ *     valid rows o.
+ * Returns the split (>= 1) or < 0. Launches only: no host synchronisation, no allocation (graph-capturable). */
+int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, const int32_t* out_rows,
+            size_t n_out, void* y, int epi, uint64_t* keys, int whole);
+
+/* Gemm::put_block (core.rs:619-657): rewrite the 16-row block `block` of an int4 matrix made by qh_mat_quant_rows
+ * with stored rows rows16[0..16) of q (zero points `zeros`), counting it as valid. Stages through the matrix's own
+ * staging buffer (allocated at upload, like Gemm::block_stage): no allocation. */
+int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros, size_t block,
+                 const size_t* rows16);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWENNY_HIP_H */

@@ -1,0 +1,153 @@
+"""CPU oracle of qwenny's quantized-weight products — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the checker
+(or the timed CPU baseline), never as the thing shipped: the product (qwenny_amd) never imports it.
+
+ctypes bindings of oracle.c (the C restatement, built by oracle/Makefile) plus numpy restatements of the small
+epilogue pieces. Every function cites the reference file:line it follows (paths relative to the reference repository).
+
+Pinning: every function is checked in tests/test_oracle.py against hand-built known answers, closed forms, library
+routines (numpy f64 matmul, torch's bf16 rounding and SiLU) or the reference's own known-answer generator
+(src/mlx/metal.rs:375-384). Nothing here is "parity unpinned".
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        _lib = ctypes.CDLL(LIB)
+        P, S, I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        _lib.or_packed_matrix.argtypes = [P, S, S, S, I, I, P, P, S, S, P, P, P, P, P]
+        _lib.or_packed_matrix.restype = I
+        _lib.or_row_into.argtypes = [I, S, S, P, P, P, S, P]
+        _lib.or_zero_points.argtypes = [I, S, P, P, P]
+        _lib.or_zero_points.restype = I
+        _lib.or_row_order.argtypes = [S, I, P]
+        _lib.or_requant_int8.argtypes = [P, S, S, P, P]
+        _lib.or_gemm_f64.argtypes = [I, S, S, S, P, P, P, P, S, P, I]
+        _lib.or_gemm_f32.argtypes = [I, S, S, S, P, P, P, P, S, P, I]
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def packed_matrix(weight_packed, weight_scale, bits, group, cols=0, zero_point=None):
+    """Checkpoint::packed_matrix (src/checkpoint.rs:408-453) -> (bits, group, cols, scales f32, offsets f32)."""
+    wp = np.ascontiguousarray(weight_packed, dtype=np.uint32)
+    rows, words = wp.shape
+    sc = np.ascontiguousarray(weight_scale, dtype=np.float32).reshape(-1)
+    zp = None if zero_point is None else np.ascontiguousarray(zero_point, dtype=np.uint32)
+    out_s = np.empty(sc.size, np.float32)
+    out_o = np.empty(sc.size, np.float32)
+    b, g, c = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_size_t()
+    rc = lib().or_packed_matrix(_p(wp), rows, words, cols, bits, group, _p(sc), _p(zp),
+                                0 if zp is None else zp.shape[0], 0 if zp is None else zp.shape[1],
+                                _p(out_s), _p(out_o), ctypes.byref(b), ctypes.byref(g), ctypes.byref(c))
+    if rc != 0:
+        raise ValueError("packed matrix does not fit compressed-tensors' packing")
+    return b.value, g.value, c.value, out_s, out_o
+
+
+def row_into(bits, group, cols, q, scales, offsets, r):
+    """Quant::row_into (src/checkpoint.rs:39-47): row r as f32."""
+    out = np.empty(cols, np.float32)
+    lib().or_row_into(bits, group, cols, _p(np.ascontiguousarray(q, np.uint32)),
+                      _p(np.ascontiguousarray(scales, np.float32)), _p(np.ascontiguousarray(offsets, np.float32)),
+                      r, _p(out))
+    return out
+
+
+def zero_points(bits, scales, offsets):
+    """Quant::zero_points (src/checkpoint.rs:72-82): uint8 array or None."""
+    s = np.ascontiguousarray(scales, np.float32).reshape(-1)
+    o = np.ascontiguousarray(offsets, np.float32).reshape(-1)
+    z = np.empty(s.size, np.uint8)
+    return z if lib().or_zero_points(bits, s.size, _p(s), _p(o), _p(z)) else None
+
+
+def row_order(rows, silu):
+    """row_order (src/cuda/core.rs:108-114)."""
+    out = np.empty(rows, np.uintp)
+    lib().or_row_order(rows, int(silu), _p(out))
+    return out.astype(np.int64)
+
+
+def requant_int8(w_bf16):
+    """Mat::new int8 branch (src/cuda/core.rs:356-369): (stored values u8 [rows][cols], scales f32 [rows][cols/128])."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    rows, cols = w.shape
+    vals = np.empty((rows, cols), np.uint8)
+    sc = np.empty((rows, cols // 128), np.float32)
+    lib().or_requant_int8(_p(w), rows, cols, _p(vals), _p(sc))
+    return vals, sc
+
+
+def gemm_f64(bits, group, q, scales, offsets, x_bf16, threads=None):
+    """y[t][r] = sum_c x[t][c] (q - z) s in f64 (src/checkpoint.rs:39-47 semantics); x bf16 bits [m][cols]."""
+    q = np.ascontiguousarray(q, np.uint32)
+    rows, words = q.shape
+    cols = words * 32 // bits
+    x = np.ascontiguousarray(x_bf16, np.uint16).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float64)
+    lib().or_gemm_f64(bits, group, rows, cols, _p(q), _p(np.ascontiguousarray(scales, np.float32)),
+                      _p(np.ascontiguousarray(offsets, np.float32)), _p(x), x.shape[0], _p(y),
+                      threads or os.cpu_count() or 1)
+    return y
+
+
+def gemm_f32(bits, group, q, scales, offsets, x_bf16, threads=1):
+    """The reference's CPU form: Quant::row_into to f32, then a plain f32 dot (the benchmark's CPU baseline)."""
+    q = np.ascontiguousarray(q, np.uint32)
+    rows, words = q.shape
+    cols = words * 32 // bits
+    x = np.ascontiguousarray(x_bf16, np.uint16).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    lib().or_gemm_f32(bits, group, rows, cols, _p(q), _p(np.ascontiguousarray(scales, np.float32)),
+                      _p(np.ascontiguousarray(offsets, np.float32)), _p(x), x.shape[0], _p(y), threads)
+    return y
+
+
+# ---- epilogues (numpy restatements) ---------------------------------------------------------------------------
+
+
+def silu_glu(y_f64, order):
+    """SwiGLU epilogue (kernels/gemm.cuh:83-91, kernels/marlin.cuh:490-492 with row_order src/cuda/core.rs:108-114):
+    y [m][rows] in ORIGINAL row order ([gate; up]) -> silu(gate) * up [m][rows/2]."""
+    del order  # the oracle works in original row order: gate rows 0..rows/2, up rows rows/2..rows
+    half = y_f64.shape[1] // 2
+    g, u = y_f64[:, :half], y_f64[:, half:]
+    return g / (1.0 + np.exp(-g)) * u
+
+
+def ordered(v):
+    """ordered() (kernels/common.cuh:60-63): order-preserving float -> u32."""
+    u = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+
+
+def argmax_keys(logits_f32, valid):
+    """The argmax key per logit row (kernels/gemm.cuh:72-74, kernels/marlin.cuh:499-517):
+    max over rows o < valid of (ordered(v) << 32) | (0xffffffff - o): the largest value, lowest index on ties."""
+    lg = np.asarray(logits_f32, np.float32)[:, :valid]
+    idx = np.arange(valid, dtype=np.uint64)
+    keys = (ordered(lg) << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)[None, :]
+    return keys.max(axis=1)

@@ -1,0 +1,306 @@
+// Device side of the C ABI (include/qwenny_hip.h): contexts, device matrices and the product dispatch by token count.
+// Mirrors the reference's Gemm / Mat runtime (cuda/core.rs:94-681) over HIP: the matrix owns its device buffers, the
+// product only launches (no allocation, no host synchronisation), errors come back as status codes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "internal.h"
+#include "kernels.h"
+#include "layout.h"
+
+using namespace qh;
+
+struct qh_ctx {
+    int device;
+    int cus;  // compute units
+};
+
+struct qh_mat {
+    int wt;
+    bool per_channel;  // int8 with one scale per row (every group's equal): exact integer prefill products
+    size_t rows, cols, valid;
+    size_t code_bytes, scale_bytes, zero_bytes;
+    void* codes;
+    void* scales;
+    void* zeros;
+    // put_block staging (one tile: codes, scales, zeros), pinned, reused after `staged` completes
+    uint8_t* stage;
+    hipEvent_t staged;
+};
+
+#define HIP_TRY(call)                                                                              \
+    do {                                                                                           \
+        hipError_t e_ = (call);                                                                    \
+        if (e_ != hipSuccess) return fail(QH_EHIP, "%s: %s", #call, hipGetErrorString(e_));        \
+    } while (0)
+
+extern "C" int qh_open(int device, qh_ctx** out) {
+    if (!out) return fail(QH_EINVAL, "open: null output");
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(QH_EINVAL, "device %d of %d", device, count);
+    HIP_TRY(hipSetDevice(device));
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    *out = new qh_ctx{device, std::max(cus, 1)};
+    return QH_OK;
+}
+
+extern "C" void qh_close(qh_ctx* ctx) { delete ctx; }
+
+static void mat_release(qh_mat* m) {
+    if (!m) return;
+    if (m->codes) (void)hipFree(m->codes);
+    if (m->scales) (void)hipFree(m->scales);
+    if (m->zeros) (void)hipFree(m->zeros);
+    if (m->stage) (void)hipHostFree(m->stage);
+    if (m->staged) (void)hipEventDestroy(m->staged);
+    delete m;
+}
+
+extern "C" void qh_mat_free(qh_mat* m) { mat_release(m); }
+
+static int mat_alloc(int wt, size_t rows, size_t cols, size_t valid, qh_mat** out) {
+    qh_mat* m = new qh_mat{};
+    m->wt = wt;
+    m->rows = rows;
+    m->cols = cols;
+    m->valid = valid;
+    if (int e = qh_packed_sizes(wt, rows, cols, &m->code_bytes, &m->scale_bytes, &m->zero_bytes)) {
+        delete m;
+        return e;
+    }
+    if (valid > rows) {
+        delete m;
+        return fail(QH_EINVAL, "%zu valid rows of %zu", valid, rows);
+    }
+    size_t tiles = rows / TILE;
+    size_t stage = (m->code_bytes + m->scale_bytes + m->zero_bytes) / tiles;
+    if (hipMalloc(&m->codes, m->code_bytes) != hipSuccess || hipMalloc(&m->scales, m->scale_bytes) != hipSuccess ||
+        (m->zero_bytes && hipMalloc(&m->zeros, m->zero_bytes) != hipSuccess) ||
+        hipHostMalloc((void**)&m->stage, stage, hipHostMallocDefault) != hipSuccess ||
+        hipEventCreateWithFlags(&m->staged, hipEventDisableTiming) != hipSuccess) {
+        mat_release(m);
+        return fail(QH_ENOMEM, "device matrix of %zu x %zu: allocation failed", rows, cols);
+    }
+    *out = m;
+    return QH_OK;
+}
+
+extern "C" int qh_mat_upload(qh_ctx* ctx, int wt, size_t rows, size_t cols, const void* codes, const void* scales,
+                             const void* zeros, size_t valid, qh_mat** out) {
+    if (!ctx || !codes || !scales || !out || (has_zeros(wt) && !zeros)) return fail(QH_EINVAL, "upload: null");
+    qh_mat* m = nullptr;
+    if (int e = mat_alloc(wt, rows, cols, valid, &m)) return e;
+    if (hipMemcpy(m->codes, codes, m->code_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->scales, scales, m->scale_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+        (m->zero_bytes && hipMemcpy(m->zeros, zeros, m->zero_bytes, hipMemcpyHostToDevice) != hipSuccess)) {
+        mat_release(m);
+        return fail(QH_EHIP, "upload of %zu x %zu failed", rows, cols);
+    }
+    if (wt == QH_WT_I8) {
+        const float* s = (const float*)scales;
+        const size_t G = cols / QG, tiles = rows / TILE;
+        m->per_channel = true;
+        for (size_t t = 0; t < tiles && m->per_channel; t++)
+            for (size_t g = 1; g < G && m->per_channel; g++)
+                m->per_channel = memcmp(s + (t * G + g) * TILE, s + t * G * TILE, TILE * sizeof(float)) == 0;
+    }
+    *out = m;
+    return QH_OK;
+}
+
+// int4 storage of q: bf16 scales when every scale is exact in bf16, else f32.
+static int int4_storage(const qh_quant* q, bool sym) {
+    const size_t n = q->rows * (q->cols / (size_t)q->group);
+    bool bf16 = true;
+    for (size_t i = 0; i < n && bf16; i++) bf16 = bf16_to_f32(f32_to_bf16(q->scales[i])) == q->scales[i];
+    if (sym) return bf16 ? QH_WT_I4 : QH_WT_I4_S32;
+    return bf16 ? QH_WT_I4Z : QH_WT_I4Z_S32;
+}
+
+// Pack `order` rows of q and upload them.
+static int pack_upload(qh_ctx* ctx, const qh_quant* q, const uint8_t* zeros, const size_t* order, size_t n, int wt,
+                       size_t valid, qh_mat** out) {
+    size_t cb, sb, zb;
+    if (int e = qh_packed_sizes(wt, n, q->cols, &cb, &sb, &zb)) return e;
+    std::vector<uint8_t> codes(cb), scales(sb), zs(zb);
+    if (int e = qh_pack_quant(q, zeros, order, n, wt, codes.data(), scales.data(), zs.data())) return e;
+    return qh_mat_upload(ctx, wt, n, q->cols, codes.data(), scales.data(), zs.data(), valid, out);
+}
+
+extern "C" int qh_mat_quant(qh_ctx* ctx, const qh_quant* q, int silu, qh_mat** out) {
+    if (!ctx || !q || !out) return fail(QH_EINVAL, "mat quant: null");
+    if (q->rows % TILE || q->cols % QG || q->group <= 0 || q->group % QG)
+        return fail(QH_ENOTFIT, "%d-bit %zu x %zu in groups of %d: rows must be a multiple of 16, columns and "
+                    "groups of 128", q->bits, q->rows, q->cols, q->group);
+    std::vector<uint8_t> z(q->rows * (q->cols / (size_t)q->group));
+    int zp = qh_quant_zero_points(q, z.data());
+    if (zp < 0) return zp;
+    if (zp == 0) return fail(QH_ENOTFIT, "%d-bit %zu x %zu: zero points are not integers", q->bits, q->rows, q->cols);
+    std::vector<size_t> order(q->rows);
+    if (int e = qh_row_order(q->rows, silu, order.data())) return e;
+    int wt;
+    if (q->bits == 8) {
+        if (std::any_of(z.begin(), z.end(), [](uint8_t v) { return v != 128; }))
+            return fail(QH_ENOTFIT, "int8 %zu x %zu: zero points other than 128", q->rows, q->cols);
+        wt = QH_WT_I8;
+    } else {
+        wt = int4_storage(q, std::all_of(z.begin(), z.end(), [](uint8_t v) { return v == 8; }));
+    }
+    return pack_upload(ctx, q, has_zeros(wt) ? z.data() : nullptr, order.data(), q->rows, wt, q->rows, out);
+}
+
+extern "C" int qh_mat_quant_rows(qh_ctx* ctx, const qh_quant* q, const uint8_t* zeros, const size_t* rows, size_t n,
+                                 size_t cap, qh_mat** out) {
+    if (!ctx || !q || !zeros || !rows || !out) return fail(QH_EINVAL, "mat rows: null");
+    if (q->bits != 4) return fail(QH_EINVAL, "int4 rows only, not %d-bit ones", q->bits);
+    if (n == 0 || n % TILE || cap % TILE || n > cap) return fail(QH_EINVAL, "%zu rows (room for %zu)", n, cap);
+    size_t nz = q->rows * (q->cols / (size_t)q->group);
+    bool sym = std::all_of(zeros, zeros + nz, [](uint8_t v) { return v == 8; });
+    std::vector<size_t> order(cap, rows[0]);
+    std::copy(rows, rows + n, order.begin());
+    const int wt = int4_storage(q, sym);
+    return pack_upload(ctx, q, has_zeros(wt) ? zeros : nullptr, order.data(), cap, wt, n, out);
+}
+
+extern "C" int qh_mat_dense_int8(qh_ctx* ctx, const uint16_t* bf16, size_t rows, size_t cols, int silu,
+                                 qh_mat** out) {
+    if (!ctx || !bf16 || !out) return fail(QH_EINVAL, "dense int8: null");
+    size_t cb, sb;
+    if (int e = qh_packed_sizes(QH_WT_I8, rows, cols, &cb, &sb, nullptr)) return e;
+    std::vector<size_t> order(rows);
+    if (int e = qh_row_order(rows, silu, order.data())) return e;
+    std::vector<uint8_t> codes(cb), scales(sb);
+    if (int e = qh_pack_dense_int8(bf16, rows, cols, order.data(), rows, codes.data(), scales.data())) return e;
+    return qh_mat_upload(ctx, QH_WT_I8, rows, cols, codes.data(), scales.data(), nullptr, rows, out);
+}
+
+extern "C" int qh_mat_describe(const qh_mat* m, qh_mat_desc* out) {
+    if (!m || !out) return fail(QH_EINVAL, "describe: null");
+    *out = qh_mat_desc{m->wt, m->rows, m->cols, m->valid, m->code_bytes, m->scale_bytes, m->zero_bytes};
+    return QH_OK;
+}
+
+extern "C" int qh_mat_download(const qh_mat* m, void* codes, void* scales, void* zeros) {
+    if (!m || !codes || !scales) return fail(QH_EINVAL, "download: null");
+    HIP_TRY(hipMemcpy(codes, m->codes, m->code_bytes, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(scales, m->scales, m->scale_bytes, hipMemcpyDeviceToHost));
+    if (zeros && m->zero_bytes) HIP_TRY(hipMemcpy(zeros, m->zeros, m->zero_bytes, hipMemcpyDeviceToHost));
+    return QH_OK;
+}
+
+// The skinny kernel's K partition: waves per workgroup and grid split for a product of m tokens. Enough waves
+// (about 16 per CU) to keep HBM busy, at least two groups per wave; non-plain epilogues need whole sums in one
+// workgroup (split 1).
+struct Partition {
+    int waves, split;
+};
+
+static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, bool plain) {
+    const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
+    const int wgs = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;
+    const int target = ctx->cus * 16;
+    int ks = std::max(1, std::min((target + wgs - 1) / wgs, std::max(1, G / 2)));
+    if (!plain) return Partition{std::min(ks, 16), 1};
+    int waves = std::min(ks, 8);
+    int split = std::max(1, std::min((ks + waves - 1) / waves, G / waves));
+    return Partition{waves, split};
+}
+
+extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
+    if (!ctx || !m) return fail(QH_EINVAL, "split: null");
+    if (n == 0 || n > (size_t)SKINNY_MAX_M) return 1;
+    return skinny_partition(ctx, m, true).split;
+}
+
+extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok) {
+    size_t len = 0;
+    for (size_t i = 0; ctx && mats && i < count; i++) {
+        if (!mats[i]) continue;
+        size_t rows = std::max(max_tok, (size_t)qh_mat_split(ctx, mats[i], 1) * std::min(max_tok, (size_t)SKINNY_MAX_M));
+        len = std::max(len, rows * mats[i]->rows);
+    }
+    return len;
+}
+
+extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
+                       const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
+    if (!ctx || !w || !x || !y) return fail(QH_EINVAL, "gemm: null");
+    if (epi != QH_EPI_PLAIN && epi != QH_EPI_SILU && epi != QH_EPI_ARGMAX) return fail(QH_EINVAL, "epilogue %d", epi);
+    if (epi == QH_EPI_ARGMAX && !keys) return fail(QH_EINVAL, "argmax without keys");
+    if (epi == QH_EPI_SILU && w->rows % 16) return fail(QH_EINVAL, "SwiGLU of %zu rows", w->rows);
+    if (ldx == 0) ldx = w->cols;
+    if (ldx < w->cols || ldx % 8 || (uintptr_t)x % 16)
+        return fail(QH_EINVAL, "x rows of %zu elements at %p: 16-byte aligned rows of at least %zu", ldx, x, w->cols);
+    const size_t m = epi == QH_EPI_ARGMAX ? n_out : n;
+    if (m == 0) return 1;
+    if (m > (1u << 24) || w->rows > (1u << 30) || ldx > (1u << 30)) return fail(QH_EINVAL, "gemm: sizes too large");
+    Launch l{};
+    l.codes = w->codes;
+    l.scales = w->scales;
+    l.zeros = (const uint64_t*)w->zeros;
+    l.fmt = (is_i8(w->wt) ? F_I8 | (w->per_channel ? F_PERCH : 0) : 0) | (has_zeros(w->wt) ? F_ZP : 0) |
+            (f32_scales(w->wt) ? F_S32 : 0);
+    l.rows = (int)w->rows;
+    l.cols = (int)w->cols;
+    l.valid = (int)w->valid;
+    l.x = x;
+    l.ldx = (int)ldx;
+    l.xrows = epi == QH_EPI_ARGMAX ? out_rows : nullptr;
+    l.m = (int)m;
+    l.y = y;
+    l.ldy = (int)(epi == QH_EPI_SILU ? w->rows / 2 : w->rows);
+    l.keys = (unsigned long long*)keys;
+    l.epi = epi;
+    l.stream = (hipStream_t)stream;
+    if (m <= (size_t)SKINNY_MAX_M) {
+        Partition p = skinny_partition(ctx, w, epi == QH_EPI_PLAIN && !whole);
+        l.waves = p.waves;
+        l.split = p.split;
+    } else {
+        l.waves = 4;
+        l.split = 1;
+    }
+    hipError_t e = launch(l);
+    if (e != hipSuccess) return fail(QH_EHIP, "gemm launch: %s", hipGetErrorString(e));
+    return l.split;
+}
+
+extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros,
+                            size_t block, const size_t* rows16) {
+    if (!ctx || !m || !q || !zeros || !rows16) return fail(QH_EINVAL, "put block: null");
+    if (is_i8(m->wt) || q->bits != 4) return fail(QH_EINVAL, "put block: int4 matrices only");
+    if (q->cols != m->cols || (block + 1) * TILE > m->rows)
+        return fail(QH_EINVAL, "block %zu of a matrix of %zu rows", block, m->rows);
+    const size_t qgroups = q->cols / (size_t)q->group;
+    for (int r = 0; r < TILE; r++) {
+        if (rows16[r] >= q->rows) return fail(QH_EINVAL, "put block: row %zu of %zu", rows16[r], q->rows);
+        if (!has_zeros(m->wt))
+            for (size_t g = 0; g < qgroups; g++)
+                if (zeros[rows16[r] * qgroups + g] != 8)
+                    return fail(QH_EINVAL, "rows with zero points for a symmetric matrix");
+    }
+    const size_t tiles = m->rows / TILE;
+    const size_t cb = m->code_bytes / tiles, sb = m->scale_bytes / tiles, zb = m->zero_bytes / tiles;
+    HIP_TRY(hipEventSynchronize(m->staged));  // the previous block's copies have left the staging buffer
+    uint8_t* st = m->stage;
+    if (!f32_scales(m->wt))
+        for (int r = 0; r < TILE; r++)
+            for (size_t g = 0; g < qgroups; g++) {
+                const float sc = q->scales[rows16[r] * qgroups + g];
+                if (bf16_to_f32(f32_to_bf16(sc)) != sc)
+                    return fail(QH_EINVAL, "put block: a scale bf16 does not hold in a bf16-scaled matrix");
+            }
+    if (int e = qh_pack_quant(q, has_zeros(m->wt) ? zeros : nullptr, rows16, TILE, m->wt, st, st + cb, st + cb + sb))
+        return e;
+    hipStream_t s = (hipStream_t)stream;
+    HIP_TRY(hipMemcpyAsync((uint8_t*)m->codes + block * cb, st, cb, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync((uint8_t*)m->scales + block * sb, st + cb, sb, hipMemcpyHostToDevice, s));
+    if (zb) HIP_TRY(hipMemcpyAsync((uint8_t*)m->zeros + block * zb, st + cb + sb, zb, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(m->staged, s));
+    m->valid = std::max(m->valid, (block + 1) * TILE);
+    return QH_OK;
+}

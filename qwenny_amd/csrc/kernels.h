@@ -1,0 +1,46 @@
+// Launch interface of the product kernels (kernels.hip), used by the C ABI (api.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qh {
+
+// Kernel storage format: bit flags. int4 symmetric with bf16 scales is F_I4 (0).
+enum {
+    F_I4 = 0,
+    F_I8 = 1,     // int8 codes (stored q + 128), 2 KiB blocks
+    F_ZP = 2,     // int4 with zero points
+    F_S32 = 4,    // f32 scales (else bf16)
+    F_PERCH = 8,  // int8 with one scale per row: exact integer weights, the row's scale after the sum
+};
+
+struct Launch {
+    const void* codes;
+    const void* scales;
+    const uint64_t* zeros;  // F_ZP only
+    int fmt;                // F_* flags
+    int rows;               // packed rows (outputs), multiple of 16
+    int cols;               // K, multiple of 128
+    int valid;              // rows that count for the argmax
+    const void* x;          // bf16 activations
+    int ldx;                // elements between x rows
+    const int32_t* xrows;   // x row of token t (argmax logit rows), or null: t
+    int m;                  // tokens
+    void* y;
+    int ldy;                // elements between y rows
+    unsigned long long* keys;
+    int epi;                // enum qh_epi
+    int split;              // grid split-K (plain products only)
+    int waves;              // waves per workgroup, splitting K inside it (skinny kernel)
+    hipStream_t stream;
+};
+
+// Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
+constexpr int SKINNY_MAX_M = 16;
+// 16-row tiles per wave in the skinny kernel.
+constexpr int SKINNY_TILES = 2;
+
+// The skinny kernel for m <= SKINNY_MAX_M, else the prefill kernel.
+hipError_t launch(const Launch& l);
+
+}  // namespace qh

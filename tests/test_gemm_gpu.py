@@ -1,0 +1,116 @@
+"""Parity of the HIP products with the oracle (dequantize-then-matmul in f64), through the C ABI.
+
+Bar: max |err| <= 2e-2 * RMS(output) (bf16 operands, f32 accumulation); bf16 outputs (SwiGLU) may differ by one
+more bf16 ulp of the value. Beyond the bar, each kernel is pinned to its own arithmetic: the skinny kernel multiplies
+exact integers by bf16 activations and applies scales in f32, so it matches the f64 oracle to 1e-4; the prefill kernel
+rounds each dequantized weight (q - z) s to bf16 once, so it matches an f64 product of bf16-rounded weights to 1e-4
+(per-channel int8 keeps exact integer weights and matches the oracle itself).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from qwenny_amd import Epi, Mat, Wt, row_order
+from qwenny_amd.synth import activations, bf16_to_f32
+from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, sub_quant,
+                           to_dev)
+
+pytestmark = pytest.mark.gpu
+
+KINDS = ["i4", "i4z", "i8"]
+WT_OF = {"i4": Wt.I4, "i4z": Wt.I4Z, "i8": Wt.I8}
+
+
+def _plain(gemm, mat, x, m, stream=None):
+    import torch
+
+    split = mat.split(m) if m <= 16 else 1
+    y = torch.full((split, m, mat.rows), float("nan"), dtype=torch.float32, device="cuda")
+    got = gemm.run(stream, m, mat, to_dev(x), y, Epi.Plain)
+    torch.cuda.synchronize()
+    assert got == split
+    return y.sum(0).cpu().numpy().astype(np.float64)
+
+
+def _check(got, q, x, m):
+    """The bar against the oracle, and the kernel's own arithmetic to 1e-4."""
+    want = oracle_y(q, x)
+    err = rel_err(got, want)
+    assert err <= TOL, f"max|err|/rms {err:.3e} vs the oracle"
+    exact = want if m <= 16 else emulate_bf16_weights(q, x)
+    err = rel_err(got, exact)
+    assert err <= 1e-4, f"max|err|/rms {err:.3e} vs the kernel's arithmetic"
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16])
+def test_skinny_plain(gemm, kind, m):
+    print(f"skinny plain {kind} m={m}", flush=True)
+    q = make_quant(11 + m, kind, 512, 1024)
+    x = activations(5 + m, "x", m, 1024)
+    mat = Mat.stack(gemm, [q])
+    assert mat.wt == WT_OF[kind]
+    _check(_plain(gemm, mat, x, m), q, x, m)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("m", [17, 64, 130, 256, 300])
+def test_prefill_plain(gemm, kind, m):
+    print(f"prefill plain {kind} m={m}", flush=True)
+    q = make_quant(21 + m, kind, 384, 768)
+    x = activations(6 + m, "x", m, 768, outliers=0.01)
+    mat = Mat.stack(gemm, [q])
+    _check(_plain(gemm, mat, x, m), q, x, m)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("m", [1, 5, 40, 300])
+def test_silu(gemm, kind, m):
+    import torch
+
+    print(f"silu {kind} m={m}", flush=True)
+    n, k = 512, 512
+    gate = make_quant(31, kind, n // 2, k)
+    up = make_quant(32, kind, n // 2, k)
+    x = activations(7, "x", m, k)
+    mat = Mat.stack(gemm, [gate, up], silu=True)
+    y = torch.full((m, n // 2), float("nan"), dtype=torch.bfloat16, device="cuda")
+    assert gemm.run(None, m, mat, to_dev(x), y, Epi.Silu) == 1
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1)
+    want = oracle.silu_glu(full, row_order(n, True))
+    assert bf16_out_err(got, want) <= TOL
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n_out", [1, 3, 16, 40])
+def test_argmax(gemm, kind, n_out):
+    import torch
+
+    print(f"argmax {kind} n_out={n_out}", flush=True)
+    n, k, steps = 1024, 512, 50
+    q = make_quant(41, kind, n, k)
+    x = activations(8, "x", steps, k)
+    rows = np.random.default_rng(3).choice(steps, n_out, replace=False).astype(np.int32)
+    mat = Mat.stack(gemm, [q])
+    y = torch.zeros((n_out, n), dtype=torch.float32, device="cuda")
+    keys = torch.zeros(n_out, dtype=torch.int64, device="cuda")
+    out_rows = torch.from_numpy(rows).cuda()
+    gemm.run(None, steps, mat, to_dev(x), y, Epi.Argmax, out_rows=out_rows, n_out=n_out, keys=keys)
+    torch.cuda.synchronize()
+    want = oracle_y(q, x[rows])
+    got = y.cpu().numpy()
+    assert rel_err(got, want) <= TOL
+    # the keys are exactly those of the logits the kernel wrote
+    assert (keys.cpu().numpy().view(np.uint64) == oracle.argmax_keys(got, n)).all()
+    assert (np.argmax(want, axis=1) == np.argmax(got, axis=1)).all()
+
+
+def test_skinny_baseline_shape(gemm):
+    """M=1, K=2560, N=9728, symmetric."""
+    q = make_quant(1, "i4", 9728, 2560)
+    x = activations(1, "x", 1, 2560)
+    mat = Mat.stack(gemm, [q])
+    assert rel_err(_plain(gemm, mat, x, 1), oracle_y(q, x)) <= 1e-4

@@ -1,0 +1,240 @@
+"""Pins of the CPU oracle (oracle/) against hand-built known answers, closed forms, library routines and the
+reference's own known-answer generator — so that the oracle is checked against something other than itself."""
+
+import numpy as np
+import pytest
+
+import oracle
+from qwenny_amd.synth import bf16_to_f32, f32_to_bf16
+
+# ---- Checkpoint::packed_matrix (src/checkpoint.rs:408-453) and Quant::row_into (:39-47) ---------------------------
+
+
+def test_packed_matrix_symmetric_known_values():
+    # one row of 16 int4 values 0..15: value c in word c / 8 at bits 4 (c % 8) (src/checkpoint.rs:26)
+    words = np.array([[0x76543210, 0xFEDCBA98]], np.uint32)
+    scale = np.array([[0.5, 0.25]], np.float32)  # groups of 8 columns
+    bits, group, cols, sc, off = oracle.packed_matrix(words, scale, 4, 8)
+    assert (bits, group, cols) == (4, 8, 16)
+    assert off.tolist() == [-4.0, -2.0]  # zero point 2^(bits-1) = 8
+    row = oracle.row_into(bits, group, cols, words, sc, off, 0)
+    want = [(c - 8) * 0.5 for c in range(8)] + [(c - 8) * 0.25 for c in range(8, 16)]
+    assert row.tolist() == want
+
+
+def test_packed_matrix_bits_from_shape():
+    # 2 words for 8 columns: 8-bit values whatever the config says (src/checkpoint.rs:413)
+    words = np.array([[0x04030201, 0x807F0000]], np.uint32)
+    bits, group, cols, sc, off = oracle.packed_matrix(words, np.ones((1, 1), np.float32), 4, 0, cols=8)
+    assert (bits, group, cols) == (8, 8, 8)
+    row = oracle.row_into(bits, group, cols, words, sc, off, 0)
+    assert row.tolist() == [1 - 128, 2 - 128, 3 - 128, 4 - 128, -128, -128, 127 - 128, 128 - 128]
+
+
+def test_packed_matrix_zero_points_along_rows():
+    # 9 rows, 2 groups: zero points packed 8 per word along the rows -> words [2][2]
+    z = np.arange(18, dtype=np.uint32).reshape(9, 2) % 16
+    zp = np.zeros((2, 2), np.uint32)
+    for r in range(9):
+        for g in range(2):
+            zp[r // 8, g] |= z[r, g] << (4 * (r % 8))
+    words = np.zeros((9, 2), np.uint32)
+    scale = np.full((9, 2), 2.0, np.float32)
+    _, _, _, sc, off = oracle.packed_matrix(words, scale, 4, 8, zero_point=zp)
+    assert off.reshape(9, 2).tolist() == (-2.0 * z).tolist()
+
+
+def test_packed_matrix_zero_points_along_groups():
+    # 2 rows, 9 groups of 8: zero points packed along each row's groups -> words [2][2]
+    z = (np.arange(18, dtype=np.uint32).reshape(2, 9) * 7) % 16
+    zp = np.zeros((2, 2), np.uint32)
+    for r in range(2):
+        for g in range(9):
+            zp[r, g // 8] |= z[r, g] << (4 * (g % 8))
+    words = np.zeros((2, 9), np.uint32)
+    _, _, _, sc, off = oracle.packed_matrix(words, np.ones((2, 9), np.float32), 4, 8, zero_point=zp)
+    assert off.reshape(2, 9).tolist() == (-1.0 * z).tolist()
+
+
+def test_packed_matrix_bad_zero_point_shape():
+    with pytest.raises(ValueError):
+        oracle.packed_matrix(np.zeros((4, 2), np.uint32), np.ones((4, 2), np.float32), 4, 8,
+                             zero_point=np.zeros((3, 3), np.uint32))
+
+
+# ---- Quant::zero_points (src/checkpoint.rs:72-82) -----------------------------------------------------------------
+
+
+def test_zero_points():
+    s = np.array([0.5, 0.25, 1e-3, 0.0], np.float32)
+    assert oracle.zero_points(4, s, -8 * s).tolist() == [8, 8, 8, 0]  # s == 0 -> z 0
+    assert oracle.zero_points(4, s[:3], -np.array([0, 15, 3], np.float32) * s[:3]).tolist() == [0, 15, 3]
+    assert oracle.zero_points(4, s[:1], np.array([-8.2], np.float32) * s[:1]) is None  # not an integer
+    assert oracle.zero_points(4, s[:1], np.array([-16.0], np.float32) * s[:1]) is None  # beyond 15
+    assert oracle.zero_points(4, s[:1], np.array([1.0], np.float32) * s[:1]) is None  # negative
+    near = np.array([-(3 + 5e-4)], np.float32) * s[:1]
+    assert oracle.zero_points(4, s[:1], near).tolist() == [3]  # within 1e-3
+    assert oracle.zero_points(8, np.ones(1, np.float32), np.array([-128.0], np.float32)).tolist() == [128]
+
+
+# ---- row_order (src/cuda/core.rs:108-114) --------------------------------------------------------------------------
+
+
+def test_row_order():
+    want = list(range(0, 8)) + list(range(16, 24)) + list(range(8, 16)) + list(range(24, 32))
+    assert oracle.row_order(32, True).tolist() == want
+    assert oracle.row_order(32, False).tolist() == list(range(32))
+    o = oracle.row_order(4096, True)
+    assert sorted(o.tolist()) == list(range(4096))
+
+
+# ---- int8 requantization (src/cuda/core.rs:356-369) ----------------------------------------------------------------
+
+
+def test_requant_int8_known():
+    w = np.zeros((2, 256), np.float32)
+    w[0, 0] = 63.5  # max of group 0 -> scale 0.5
+    w[0, 1] = 1.25  # 2.5 -> rounds half away from zero: 3
+    w[0, 2] = -1.25  # -2.5 -> -3
+    w[0, 3] = -63.5  # -127
+    w[0, 4] = 0.75  # 1.5 -> 2
+    w[1, 128] = -2.0  # group 1 of row 1: scale 2/127
+    vals, sc = oracle.requant_int8(f32_to_bf16(w))
+    assert sc[0, 0] == np.float32(63.5) / np.float32(127)
+    assert sc[0, 1] == 1.0 and sc[1, 0] == 1.0  # all-zero groups
+    assert sc[1, 1] == np.float32(2.0) / np.float32(127)
+    q = vals.astype(int) - 128
+    assert q[0, :5].tolist() == [127, 3, -3, -127, 2]
+    assert (q[0, 5:] == 0).all() and q[1, 128] == -127
+    assert vals.min() >= 1  # clamped to +-127, stored + 128
+
+
+def test_requant_int8_roundtrip_error():
+    rng = np.random.default_rng(0)
+    w = f32_to_bf16(rng.standard_normal((16, 512)).astype(np.float32))
+    vals, sc = oracle.requant_int8(w)
+    deq = (vals.astype(np.float32) - 128) * np.repeat(sc, 128, axis=1)
+    assert np.abs(deq - bf16_to_f32(w)).max() <= (np.repeat(sc, 128, axis=1) / 2 * 1.0001).max()
+
+
+# ---- products: the f64 dequantize-then-matmul --------------------------------------------------------------------
+
+
+def _rand_quant(seed, rows, cols, bits=4, group=128, zp=False):
+    rng = np.random.default_rng(seed)
+    words = rng.integers(0, 1 << 32, size=(rows, cols * bits // 32), dtype=np.uint32)
+    sc = f32_to_bf16(rng.uniform(0.002, 0.02, (rows, cols // group)).astype(np.float32))
+    z = None
+    if zp:
+        zz = rng.integers(0, 16, size=(rows, cols // group), dtype=np.uint32)
+        z = np.zeros(((rows + 7) // 8, cols // group), np.uint32)
+        for r in range(rows):
+            z[r // 8] |= zz[r] << np.uint32(4 * (r % 8))
+    b, g, c, s, o = oracle.packed_matrix(words, bf16_to_f32(sc), bits, group, zero_point=z)
+    return b, g, c, words, s, o
+
+
+def _dequant_numpy(bits, group, cols, words, s, o):
+    """An independent dequantization with numpy vector ops (not the oracle's loop)."""
+    per = 32 // bits
+    shifts = (np.arange(cols) % per) * bits
+    vals = (words[:, np.arange(cols) // per] >> shifts[None, :].astype(np.uint32)) & ((1 << bits) - 1)
+    g = np.arange(cols) // group
+    rows = words.shape[0]
+    return vals * s.reshape(rows, -1)[:, g].astype(np.float64) + o.reshape(rows, -1)[:, g].astype(np.float64)
+
+
+@pytest.mark.parametrize("bits,zp", [(4, False), (4, True), (8, False)])
+def test_gemm_f64_matches_numpy(bits, zp):
+    b, g, c, words, s, o = _rand_quant(1, 48, 512, bits, 128, zp)
+    x = f32_to_bf16(np.random.default_rng(2).standard_normal((5, c)).astype(np.float32))
+    y = oracle.gemm_f64(b, g, words, s, o, x)
+    want = bf16_to_f32(x).astype(np.float64) @ _dequant_numpy(b, g, c, words, s, o).T
+    assert np.abs(y - want).max() <= 1e-12 * np.abs(want).max()
+
+
+def test_gemm_special_cases():
+    b, g, c, words, s, o = _rand_quant(3, 32, 256)
+    deq = _dequant_numpy(b, g, c, words, s, o)
+    # one-hot x selects one column of the dequantized matrix
+    x = np.zeros((1, c), np.float32)
+    x[0, 77] = 1.0
+    assert np.array_equal(oracle.gemm_f64(b, g, words, s, o, f32_to_bf16(x))[0], deq[:, 77])
+    # every code equal to the zero point -> 0
+    eight = np.full_like(words, 0x88888888)
+    xr = f32_to_bf16(np.random.default_rng(4).standard_normal((3, c)).astype(np.float32))
+    assert (oracle.gemm_f64(b, g, eight, s, o, xr) == 0).all()
+    # s = 1, z = 0: exact integers
+    ones, zeros = np.ones_like(s), np.zeros_like(o)
+    xi = f32_to_bf16(np.random.default_rng(5).integers(-4, 5, (2, c)).astype(np.float32))
+    y = oracle.gemm_f64(b, g, words, ones, zeros, xi)
+    vals = _dequant_numpy(b, g, c, words, ones, zeros)
+    assert np.array_equal(y, bf16_to_f32(xi).astype(np.float64) @ vals.T) and (y == np.round(y)).all()
+    # linearity in x
+    x1 = f32_to_bf16(np.random.default_rng(6).integers(-3, 4, (1, c)).astype(np.float32))
+    x2 = f32_to_bf16(np.random.default_rng(7).integers(-3, 4, (1, c)).astype(np.float32))
+    x12 = f32_to_bf16(bf16_to_f32(x1) + bf16_to_f32(x2))
+    y1, y2, y12 = (oracle.gemm_f64(b, g, words, s, o, v) for v in (x1, x2, x12))
+    assert np.allclose(y1 + y2, y12, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_f32_close_to_f64():
+    b, g, c, words, s, o = _rand_quant(8, 64, 1024)
+    x = f32_to_bf16(np.random.default_rng(9).standard_normal((2, c)).astype(np.float32))
+    y64 = oracle.gemm_f64(b, g, words, s, o, x)
+    y32 = oracle.gemm_f32(b, g, words, s, o, x, threads=3)
+    assert np.abs(y32 - y64).max() <= 1e-5 * np.sqrt((y64 ** 2).mean())
+
+
+def test_mlx_known_answer_generator():
+    """The reference's closed-form generator (src/mlx/metal.rs:375-384) and its tolerance 2e-5 (1 + |want|): the
+    oracle reproduces the f64 loop of that test, recomputed here with numpy from the committed fixture's inputs."""
+    from tests.golden.make_golden import mlx_case
+
+    for m, n, k, group, bits in [(5, 64, 256, 128, 4), (1, 35, 1024, 128, 4), (8, 35, 256, 128, 8),
+                                 (3, 35, 128, 64, 4)]:
+        x16, q, sc, bi = mlx_case(m, n, k, group, bits)
+        x = x16.astype(np.float32)
+        # the oracle takes bf16 activations; use inputs exactly representable in both (the f16 values rounded)
+        xb = f32_to_bf16(x)
+        y = oracle.gemm_f64(bits, group, q, sc.astype(np.float32), bi.astype(np.float32), xb)
+        want = bf16_to_f32(xb).astype(np.float64) @ _dequant_numpy(bits, group, k, q, sc.astype(np.float32),
+                                                                    bi.astype(np.float32)).T
+        assert (np.abs(y - want) < 2e-5 * (1 + np.abs(want))).all()
+
+
+def test_golden_fixture():
+    """The committed golden vectors (tests/golden/mlx_affine.npz, written by tests/golden/make_golden.py from the
+    reference's generator) match the oracle."""
+    import os
+
+    path = os.path.join(os.path.dirname(__file__), "golden", "mlx_affine.npz")
+    d = np.load(path)
+    for i in range(int(d["count"])):
+        bits, group = int(d[f"bits{i}"]), int(d[f"group{i}"])
+        y = oracle.gemm_f64(bits, group, d[f"q{i}"], d[f"sc{i}"], d[f"bi{i}"], d[f"xb{i}"])
+        want = d[f"y{i}"]
+        assert (np.abs(y - want) < 2e-5 * (1 + np.abs(want))).all()
+
+
+# ---- epilogues --------------------------------------------------------------------------------------------------
+
+
+def test_silu_matches_torch():
+    import torch
+
+    y = np.random.default_rng(1).standard_normal((3, 64)) * 4
+    got = oracle.silu_glu(y, None)
+    t = torch.from_numpy(y)
+    want = (torch.nn.functional.silu(t[:, :32]) * t[:, 32:]).numpy()
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_argmax_keys():
+    lg = np.array([[1.0, 3.0, 3.0, -1.0], [-2.0, -1.0, -5.0, -1.0], [0.0, -0.0, 0.0, 7.0]], np.float32)
+    keys = oracle.argmax_keys(lg, 3)  # row 2's 7.0 is past `valid`
+    idx = 0xFFFFFFFF - (keys & 0xFFFFFFFF)
+    assert idx.tolist() == [1, 1, 0]  # ties -> lowest index; -0.0 < +0.0 in the total order
+    v = np.array([-np.inf, -3.0, -1e-30, -0.0, 0.0, 1e-30, 2.0, np.inf], np.float32)
+    o = oracle.ordered(v)
+    assert (np.diff(o.astype(np.int64)) > 0).all()
