@@ -31,24 +31,27 @@ def _run(cmd):
         sys.stderr.write(err + "\n")
 
 
-def build(verbose=False):
+def build(verbose=False, out=LIB, defines=()):
+    """Compile and link the library into `out`; `defines`: extra -D macros (tuning experiments only)."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    os.makedirs(BUILD, exist_ok=True)
+    build_dir = BUILD if out == LIB else out + ".build"
+    os.makedirs(build_dir, exist_ok=True)
+    extra = [f"-D{d}" for d in defines]
     objs = []
     for src in HOST_SRC:
-        obj = os.path.join(BUILD, src + ".o")
+        obj = os.path.join(build_dir, src + ".o")
         _run([hipcc, *COMMON, "-ffp-contract=off", "-pthread", "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     for src in HIP_SRC:
-        obj = os.path.join(BUILD, src + ".o")
-        _run([hipcc, *COMMON, *DEVICE, "-c", "-x", "hip", os.path.join(CSRC, src), "-o", obj])
+        obj = os.path.join(build_dir, src + ".o")
+        _run([hipcc, *COMMON, *DEVICE, *extra, "-c", "-x", "hip", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
-    tmp = LIB + ".tmp"
+    tmp = out + ".tmp"
     _run([hipcc, *DEVICE, "-shared", "-pthread", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print("built", LIB)
-    return LIB
+        print("built", out)
+    return out
 
 
 if __name__ == "__main__":

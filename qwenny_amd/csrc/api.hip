@@ -3,6 +3,8 @@
 // product only launches (no allocation, no host synchronisation), errors come back as status codes.
 #include <hip/hip_runtime.h>
 
+#include <stdlib.h>
+
 #include <algorithm>
 #include <vector>
 
@@ -14,8 +16,15 @@ using namespace qh;
 
 struct qh_ctx {
     int device;
-    int cus;  // compute units
+    int cus;             // compute units
+    int skinny_max_w;       // skinny kernel: most waves per workgroup splitting K (non-plain epilogues)
+    int skinny_tile_waves;  // skinny kernel, plain products: waves per workgroup side by side over tiles
 };
+
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
 
 struct qh_mat {
     int wt;
@@ -44,7 +53,9 @@ extern "C" int qh_open(int device, qh_ctx** out) {
     HIP_TRY(hipSetDevice(device));
     int cus = 0;
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-    *out = new qh_ctx{device, std::max(cus, 1)};
+    // QH_SKINNY_MAX_W / QH_SKINNY_TILE_WAVES override the skinny partition (tuning sweeps)
+    *out = new qh_ctx{device, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
+                      std::min(16, std::max(1, env_int("QH_SKINNY_TILE_WAVES", 4)))};
     return QH_OK;
 }
 
@@ -105,8 +116,9 @@ extern "C" int qh_mat_upload(qh_ctx* ctx, int wt, size_t rows, size_t cols, cons
         const size_t G = cols / QG, tiles = rows / TILE;
         m->per_channel = true;
         for (size_t t = 0; t < tiles && m->per_channel; t++)
-            for (size_t g = 1; g < G && m->per_channel; g++)
-                m->per_channel = memcmp(s + (t * G + g) * TILE, s + t * G * TILE, TILE * sizeof(float)) == 0;
+            for (int r = 0; r < TILE && m->per_channel; r++)
+                for (size_t g = 1; g < G && m->per_channel; g++)
+                    m->per_channel = s[scale_idx(t, G, g, r)] == s[scale_idx(t, G, 0, r)];
     }
     *out = m;
     return QH_OK;
@@ -193,27 +205,39 @@ extern "C" int qh_mat_download(const qh_mat* m, void* codes, void* scales, void*
 }
 
 // The skinny kernel's K partition: waves per workgroup and grid split for a product of m tokens. Enough waves
-// (about 16 per CU) to keep HBM busy, at least two groups per wave; non-plain epilogues need whole sums in one
-// workgroup (split 1).
+// (about 12 per CU) to keep HBM busy, at least a few groups per wave so that its pipeline fills; non-plain epilogues
+// need whole sums in one workgroup (split 1).
 struct Partition {
-    int waves, split;
+    int tile_waves, waves, split, groups_per_wave;
 };
 
-static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, bool plain) {
+// The skinny kernel's partition of a product of m tokens (kernels.hip skinny_kernel): each wave takes SKINNY_TILES
+// tiles and 4 groups (1 when the group count is not a multiple of 4). Plain products: workgroups of 4 waves side by
+// side over tiles, the grid split over every chunk of K (split-K partials the consumer sums). Other epilogues need
+// whole sums in one workgroup: its waves split K (reduced through LDS), as many as divide the groups evenly and let
+// the super-chunk's activations fit in LDS; longer K is walked in super-chunks.
+static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tokens, bool plain) {
     const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
-    const int wgs = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;
-    const int target = ctx->cus * 16;
-    int ks = std::max(1, std::min((target + wgs - 1) / wgs, std::max(1, G / 2)));
-    if (!plain) return Partition{std::min(ks, 16), 1};
-    int waves = std::min(ks, 8);
-    int split = std::max(1, std::min((ks + waves - 1) / waves, G / waves));
-    return Partition{waves, split};
+    const int cols = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;  // wave columns over the tiles
+    const int ng = G % 4 == 0 ? 4 : 1;
+    if (plain) {
+        const int wt = std::max(1, std::min(ctx->skinny_tile_waves, cols));
+        return Partition{wt, wt, G / ng, ng};
+    }
+    const size_t per_group = (size_t)std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's x
+    int wk = 1;
+    for (int w = std::min(ctx->skinny_max_w, G / ng); w >= 1; w--)
+        if ((G / ng) % w == 0 && (size_t)w * ng * per_group <= SKINNY_X_LDS) {
+            wk = w;
+            break;
+        }
+    return Partition{1, wk, 1, ng};
 }
 
 extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
     if (!ctx || !m) return fail(QH_EINVAL, "split: null");
     if (n == 0 || n > (size_t)SKINNY_MAX_M) return 1;
-    return skinny_partition(ctx, m, true).split;
+    return skinny_partition(ctx, m, n, true).split;
 }
 
 extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok) {
@@ -241,7 +265,7 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     Launch l{};
     l.codes = w->codes;
     l.scales = w->scales;
-    l.zeros = (const uint64_t*)w->zeros;
+    l.zeros = (const uint16_t*)w->zeros;
     l.fmt = (is_i8(w->wt) ? F_I8 | (w->per_channel ? F_PERCH : 0) : 0) | (has_zeros(w->wt) ? F_ZP : 0) |
             (f32_scales(w->wt) ? F_S32 : 0);
     l.rows = (int)w->rows;
@@ -256,11 +280,16 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     l.keys = (unsigned long long*)keys;
     l.epi = epi;
     l.stream = (hipStream_t)stream;
+    l.bf16_magic = 0x43004300u;
+    l.nib_mask = 0x000F000Fu;
     if (m <= (size_t)SKINNY_MAX_M) {
-        Partition p = skinny_partition(ctx, w, epi == QH_EPI_PLAIN && !whole);
+        Partition p = skinny_partition(ctx, w, m, epi == QH_EPI_PLAIN && !whole);
+        l.tile_waves = p.tile_waves;
         l.waves = p.waves;
         l.split = p.split;
+        l.groups_per_wave = p.groups_per_wave;
     } else {
+        l.tile_waves = 4;
         l.waves = 4;
         l.split = 1;
     }

@@ -148,10 +148,10 @@ extern "C" int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_by
     if (!valid_wt(wt)) return fail(QH_EINVAL, "storage %d", wt);
     if (rows == 0 || rows % TILE || cols == 0 || cols % QG)
         return fail(QH_EINVAL, "%zu x %zu: rows must be a multiple of 16, columns of 128", rows, cols);
-    size_t blocks = rows / TILE * (cols / QG);
+    size_t tiles = rows / TILE, blocks = tiles * (cols / QG), qd = tiles * quads(cols / QG);
     if (code_bytes) *code_bytes = blocks * block_bytes(wt);
-    if (scale_bytes) *scale_bytes = blocks * TILE * (f32_scales(wt) ? 4 : 2);
-    if (zero_bytes) *zero_bytes = has_zeros(wt) ? blocks * 8 : 0;
+    if (scale_bytes) *scale_bytes = qd * TILE * 4 * (f32_scales(wt) ? 4 : 2);
+    if (zero_bytes) *zero_bytes = has_zeros(wt) ? qd * TILE * 2 : 0;
     return QH_OK;
 }
 
@@ -161,7 +161,7 @@ extern "C" int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_by
 template <class Word, class Scale, class Zero>
 static void pack_tile(int wt, size_t cols, const size_t* rows16, size_t t, Word word, Scale scale, Zero zero,
                       void* codes, void* scales, void* zeros) {
-    size_t G = cols / QG;
+    const size_t G = cols / QG;
     for (size_t g = 0; g < G; g++) {
         size_t blk = t * G + g;
         if (is_i8(wt)) {
@@ -172,8 +172,6 @@ static void pack_tile(int wt, size_t cols, const size_t* rows16, size_t t, Word 
                         size_t k = g * QG + 32 * (2 * h + w / 2) + 8 * (l / 16) + 4 * (w % 2);
                         out[(h * LANES + l) * 4 + w] = word(rows16[l % 16], k);
                     }
-            float* s = (float*)scales + blk * TILE;
-            for (int r = 0; r < TILE; r++) s[r] = scale(rows16[r], g);
         } else {
             uint32_t* out = (uint32_t*)codes + blk * 256;
             for (int l = 0; l < LANES; l++)
@@ -182,19 +180,24 @@ static void pack_tile(int wt, size_t cols, const size_t* rows16, size_t t, Word 
                     for (int c = 0; c < 8; c++) dst |= ((src >> (4 * c)) & 15u) << (4 * nib_pos(c));
                     out[l * 4 + j] = dst;
                 }
-            for (int r = 0; r < TILE; r++) {
-                if (f32_scales(wt))
-                    ((float*)scales)[blk * TILE + r] = scale(rows16[r], g);
-                else
-                    ((uint16_t*)scales)[blk * TILE + r] = f32_to_bf16(scale(rows16[r], g));
-            }
-            if (has_zeros(wt)) {
-                uint64_t z = 0;
-                for (int r = 0; r < TILE; r++) z |= (uint64_t)(zero(rows16[r], g) & 15u) << (4 * r);
-                ((uint64_t*)zeros)[blk] = z;
-            }
         }
     }
+    // scales and zero points by quads of 4 groups; the padding past G holds zeros
+    for (size_t g = 0; g < quads(G) * 4; g++)
+        for (int r = 0; r < TILE; r++) {
+            const float sc = g < G ? scale(rows16[r], g) : 0.0f;
+            if (f32_scales(wt))
+                ((float*)scales)[scale_idx(t, G, g, r)] = sc;
+            else
+                ((uint16_t*)scales)[scale_idx(t, G, g, r)] = f32_to_bf16(sc);
+        }
+    if (has_zeros(wt))
+        for (size_t q4 = 0; q4 < quads(G); q4++)
+            for (int r = 0; r < TILE; r++) {
+                uint16_t z = 0;
+                for (size_t g = 4 * q4; g < std::min(G, 4 * q4 + 4); g++) z |= (uint16_t)((zero(rows16[r], g) & 15u) << (4 * (g % 4)));
+                ((uint16_t*)zeros)[zero_idx(t, G, 4 * q4, r)] = z;
+            }
 }
 
 extern "C" int qh_pack_quant(const qh_quant* q, const uint8_t* zeros, const size_t* order, size_t n, int wt,
@@ -248,9 +251,11 @@ extern "C" int qh_unpack_row(int wt, size_t rows, size_t cols, const void* codes
                 }
             }
         }
-        sc[g] = f32_scales(wt) ? ((const float*)scales)[blk * TILE + r]
-                               : bf16_to_f32(((const uint16_t*)scales)[blk * TILE + r]);
-        z[g] = is_i8(wt) ? 128 : has_zeros(wt) ? (uint8_t)((((const uint64_t*)zeros)[blk] >> (4 * r)) & 15u) : 8;
+        sc[g] = f32_scales(wt) ? ((const float*)scales)[scale_idx(t, G, g, r)]
+                               : bf16_to_f32(((const uint16_t*)scales)[scale_idx(t, G, g, r)]);
+        z[g] = is_i8(wt)       ? 128
+               : has_zeros(wt) ? (uint8_t)((((const uint16_t*)zeros)[zero_idx(t, G, g, r)] >> (4 * (g % 4))) & 15u)
+                               : 8;
     }
     return QH_OK;
 }

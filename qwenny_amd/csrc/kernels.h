@@ -17,7 +17,7 @@ enum {
 struct Launch {
     const void* codes;
     const void* scales;
-    const uint64_t* zeros;  // F_ZP only
+    const uint16_t* zeros;  // F_ZP only
     int fmt;                // F_* flags
     int rows;               // packed rows (outputs), multiple of 16
     int cols;               // K, multiple of 128
@@ -31,14 +31,26 @@ struct Launch {
     unsigned long long* keys;
     int epi;                // enum qh_epi
     int split;              // grid split-K (plain products only)
-    int waves;              // waves per workgroup, splitting K inside it (skinny kernel)
+    int waves;              // waves per workgroup (skinny kernel): tile_waves over tiles x waves / tile_waves over K
+    int tile_waves;
+    int groups_per_wave;    // skinny kernel: 4, or 1 when the group count is not a multiple of 4
+    uint32_t bf16_magic;    // 0x43004300: the bf16 pair (128, 128) (see kernels.hip i4_biased)
+    uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;
 };
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
 constexpr int SKINNY_MAX_M = 16;
-// 16-row tiles per wave in the skinny kernel.
-constexpr int SKINNY_TILES = 2;
+// 16-row tiles per wave in the skinny kernel, and its pipeline depth (groups whose loads are in flight + 1).
+#ifndef QH_SKINNY_TILES
+#define QH_SKINNY_TILES 2
+#endif
+constexpr int SKINNY_TILES = QH_SKINNY_TILES;
+// Most bytes of LDS the skinny kernel stages activations in.
+constexpr size_t SKINNY_X_LDS = 64 * 1024;
+
+// Dynamic LDS of a skinny launch: the staged activations and the K reduction.
+size_t skinny_lds(const Launch& l);
 
 // The skinny kernel for m <= SKINNY_MAX_M, else the prefill kernel.
 hipError_t launch(const Launch& l);

@@ -35,13 +35,16 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
 }
 
-// int4 word (layout.h nibble order) -> bf16 (128 + q) of columns 0..7
-__device__ __forceinline__ bf16x8 i4_biased(uint32_t w) {
+// int4 word (layout.h nibble order) -> bf16 (128 + q) of columns 0..7: each 16-bit half's nibble put under the
+// exponent of 128 by one and-or (v_and_or_b32) per pair: 3 shifts and 4 and-ors for 8 values. The mask (0x000F000F)
+// and the bf16 pair (128, 128) = 0x43004300 come from the host: with both known, the compiler would split each and-or
+// into an and and an or (a gfx9 VOP3 instruction takes no literal).
+__device__ __forceinline__ bf16x8 i4_biased(uint32_t w, uint32_t mask, uint32_t magic) {
     u32x4 v;
-    v.x = (w & 0x000F000Fu) | 0x43004300u;
-    v.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-    v.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-    v.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    v.x = (w & mask) | magic;
+    v.y = ((w >> 4) & mask) | magic;
+    v.z = ((w >> 8) & mask) | magic;
+    v.w = ((w >> 12) & mask) | magic;
     return __builtin_bit_cast(bf16x8, v);
 }
 
@@ -111,59 +114,56 @@ struct CodeWords {
     static constexpr int N = (F & F_I8) ? 2 : 1;
 };
 
+// The scale and zero point of row r of `tile`, group g (G groups; layout.h scale_idx / zero_idx)
 template <int F>
-__device__ __forceinline__ float scale_of(const void* scales, size_t blk, int r) {
-    if (F & F_S32) return ((const float*)scales)[blk * TILE + r];
-    return bf16_bits_f(((const uint16_t*)scales)[blk * TILE + r]);
+__device__ __forceinline__ float scale_of(const void* scales, int tile, int G, int g, int r) {
+    if (F & F_S32) return ((const float*)scales)[scale_idx(tile, G, g, r)];
+    return bf16_bits_f(((const uint16_t*)scales)[scale_idx(tile, G, g, r)]);
 }
 
 template <int F>
-__device__ __forceinline__ int zero_of(const uint64_t* zeros, size_t blk, int r) {
-    if (F & F_ZP) return (int)((zeros[blk] >> (4 * r)) & 15u);
+__device__ __forceinline__ int zero_of(const uint16_t* zeros, int tile, int G, int g, int r) {
+    if (F & F_ZP) return (int)((zeros[zero_idx(tile, G, g, r)] >> (4 * (g & 3))) & 15u);
     return (F & F_I8) ? 128 : 8;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // skinny_kernel
+//
+// A wave owns T tiles and NG consecutive groups (one "chunk"): it issues all of that chunk's loads at once (its
+// scales, one load per tile for 4 groups, then the codes), so that many short waves keep HBM saturated, and computes
+// them as they arrive. The workgroup's waves are WT side by side over tiles times WK over consecutive chunks of K;
+// together they cover a super-chunk of CH = WK * NG groups, whose activations the workgroup stages once in LDS
+// (every wave of it reads them with ds_read_b128 instead of fetching them from L2). The grid's y dimension splits the
+// super-chunks of K (plain products: split-K partials); WK waves' partial sums are reduced through LDS.
 
-template <int F, int T>
-struct SkinnyFrag {
-    u32x4 c[T][CodeWords<F>::N];
-    float s[T];
-    float cz[T];  // 128 + zero point
-    u32x4 xa[4];
-};
+// activation pieces (16 bytes) each thread loads ahead of the weights
+constexpr int XPT = 1;
 
-template <int F, int EPI, int NR, int T>
+template <int F, int EPI, int NR, int T, int NG>
 __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
-    extern __shared__ float red[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int CW = CodeWords<F>::N;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nthr = blockDim.x, WT = a.tile_waves, WK = (nthr >> 6) / WT, wt = wave % WT, wk = wave / WT;
     const int l16 = lane & 15, kq = lane >> 4;
-    const int tiles = a.rows / TILE, G = a.cols / QG, S = a.split, M = a.m;
-    const int tile0 = blockIdx.x * T, sp = blockIdx.y;
-    const int gs0 = (int)((long)sp * G / S), gs1 = (int)((long)(sp + 1) * G / S);
-    const int g0 = gs0 + wave * (gs1 - gs0) / W, g1 = gs0 + (wave + 1) * (gs1 - gs0) / W;
+    const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
+    const int CH = WK * NG, NC = G / CH;  // groups per super-chunk, super-chunks in K
+    const int c0 = (int)((long)blockIdx.y * NC / a.split), c1 = (int)((long)(blockIdx.y + 1) * NC / a.split);
+    const int tile0 = (blockIdx.x * WT + wt) * T;
+    const int xpitch = CH * QG + 8;  // bf16 per staged x row (+16 bytes: rows start 4 banks apart)
+    __bf16* xs_lds = (__bf16*)smem;
+    float* red = (float*)(smem + (((size_t)M * xpitch * 2 + 15) & ~(size_t)15));
 
-    // this lane's x row (A operand: token l16, columns 8 kq .. 8 kq + 7 of each k32 step)
-    const __bf16* xr = nullptr;
-    if (l16 < M) xr = (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[l16] : l16) * a.ldx + 8 * kq;
-    size_t tb[T];
+    int tt[T];
 #pragma unroll
-    for (int t = 0; t < T; t++) tb[t] = (size_t)min(tile0 + t, tiles - 1) * G;
+    for (int t = 0; t < T; t++) tt[t] = min(tile0 + t, tiles - 1);
+    const int xtok = min(l16, M - 1);  // lanes of tokens past M read row M - 1: their results are never stored
 
-    auto load = [&](int g, SkinnyFrag<F, T>& f) {
-#pragma unroll
-        for (int t = 0; t < T; t++) {
-            size_t blk = tb[t] + g;
-            const u32x4* cp = (const u32x4*)a.codes + blk * 64 * CodeWords<F>::N;
-#pragma unroll
-            for (int h = 0; h < CodeWords<F>::N; h++) f.c[t][h] = __builtin_nontemporal_load(cp + h * 64 + lane);
-            f.s[t] = scale_of<F>(a.scales, blk, l16);
-            f.cz[t] = (float)(128 + ((F & F_I8) ? 0 : zero_of<F>(a.zeros, blk, l16)));
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) f.xa[j] = xr ? *(const u32x4*)(xr + (size_t)g * QG + 32 * j) : u32x4{0, 0, 0, 0};
-    };
+    const uint32_t magic_s = a.bf16_magic, mask = a.nib_mask;
+    uint32_t magic;  // in a VGPR (copied once; only VALU reads it) so that each pair is one v_and_or_b32
+    asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(magic_s));
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
     float acc[T][NR];
 #pragma unroll
@@ -171,15 +171,85 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
 #pragma unroll
         for (int r = 0; r < NR; r++) acc[t][r] = 0.0f;
 
-    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
-    if (g0 < g1) {
-        SkinnyFrag<F, T> cur, nxt;
-        load(g0, cur);
-        for (int g = g0; g < g1; g++) {
-            load(min(g + 1, g1 - 1), nxt);
-            f32x4 xs = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = c0; c < c1; c++) {
+        const int gs = c * CH;              // first group of the super-chunk
+        const int gw = gs + wk * NG;        // this wave's first group
+        // 1. the super-chunk's activations (M rows of CH * 128 columns): the first XPT pieces per thread are loaded
+        //    before the weights (loads complete in order, so staging them afterwards would wait for every weight),
+        //    the rest, if any, afterwards
+        const int rowc = CH * 16;  // 16-byte pieces per row
+        const int npieces = M * rowc;
+        u32x4 xv[XPT];
+        int xo[XPT];
 #pragma unroll
-            for (int j = 0; j < 4; j++) xs = mfma(cur.xa[j], ones, xs);
+        for (int i = 0; i < XPT; i++) {
+            const int p = threadIdx.x + i * nthr;
+            const int tok = min(p / rowc, M - 1), pc = p - (p / rowc) * rowc;
+            xo[i] = p < npieces ? tok * xpitch + 8 * pc : -1;
+            xv[i] = *(const u32x4*)((const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx +
+                                    (size_t)gs * QG + 8 * (p < npieces ? pc : 0));
+        }
+        // 2. this wave's weights: scales (4 groups per load), zero points, then codes group by group
+        uint32_t sraw[T][NG == 4 ? ((F & F_S32) ? 4 : 2) : 1];
+        uint32_t zraw[T];
+        u32x4 code[NG][T][CW];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const size_t si = scale_idx(tt[t], G, gw, l16);
+            if (NG == 4) {
+                if (F & F_S32) {
+                    const u32x4 v = *(const u32x4*)((const float*)a.scales + si);
+                    sraw[t][0] = v.x, sraw[t][1] = v.y, sraw[t][2] = v.z, sraw[t][3] = v.w;
+                } else {
+                    const uint2 v = *(const uint2*)((const uint16_t*)a.scales + si);
+                    sraw[t][0] = v.x, sraw[t][1] = v.y;
+                }
+            } else {
+                sraw[t][0] = (F & F_S32) ? ((const uint32_t*)a.scales)[si] : ((const uint16_t*)a.scales)[si];
+            }
+            if (F & F_ZP) zraw[t] = a.zeros[zero_idx(tt[t], G, gw, l16)];
+        }
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                const u32x4* cp = (const u32x4*)a.codes + ((size_t)tt[t] * G + gw + gi) * 64 * CW;
+#pragma unroll
+                for (int h = 0; h < CW; h++) code[gi][t][h] = __builtin_nontemporal_load(cp + h * 64 + lane);
+            }
+        // 3. stage the activations
+        if (c > c0) __syncthreads();  // the previous super-chunk's readers are done
+#ifndef QH_EXP_NOX
+#pragma unroll
+        for (int i = 0; i < XPT; i++)
+            if (xo[i] >= 0) *(u32x4*)(xs_lds + xo[i]) = xv[i];
+        for (int p = threadIdx.x + XPT * nthr; p < npieces; p += nthr) {
+            const int tok = p / rowc, pc = p - tok * rowc;
+            const __bf16* src =
+                (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
+            *(u32x4*)(xs_lds + (size_t)tok * xpitch + 8 * pc) = *(const u32x4*)src;
+        }
+#endif
+        __syncthreads();
+#ifdef QH_EXP_NOCOMP
+        {
+            uint32_t h = 0;
+            for (int gi = 0; gi < NG; gi++)
+                for (int t = 0; t < T; t++) h ^= code[gi][t][0].x ^ code[gi][t][0].y ^ code[gi][t][0].z ^ code[gi][t][0].w ^ sraw[t][0];
+            acc[0][0] += __uint_as_float(h & 0x3fffffffu);
+            continue;
+        }
+#endif
+        // 3. compute the wave's groups
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            const __bf16* xrow = xs_lds + (size_t)xtok * xpitch + (wk * NG + gi) * QG + 8 * kq;
+            u32x4 xa[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow + 32 * j);
+            f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -187,35 +257,48 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
                 for (int j = 0; j < 4; j++) {
                     bf16x8 b;
                     if (F & F_I8)
-                        b = i8_biased(cur.c[t][j >> 1][2 * (j & 1)], cur.c[t][j >> 1][2 * (j & 1) + 1]);
+                        b = i8_biased(code[gi][t][j >> 1][2 * (j & 1)], code[gi][t][j >> 1][2 * (j & 1) + 1]);
                     else
-                        b = i4_biased(cur.c[t][0][j]);
-                    d = mfma(cur.xa[j], b, d);
+                        b = i4_biased(code[gi][t][0][j], mask, magic);
+                    d = mfma(xa[j], b, d);
                 }
+                const int g = gw + gi;
+                // the group's scale from the raw scale words: f32 one per word; bf16 two per word (NG == 4) or one
+                float sc;
+                if (F & F_S32) {
+                    sc = __uint_as_float(sraw[t][NG == 4 ? gi : 0]);
+                } else if (NG == 4) {
+                    const uint32_t w = sraw[t][gi >> 1];
+                    sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
+                } else {
+                    sc = __uint_as_float(sraw[t][0] << 16);
+                }
+                const float cz = (F & F_ZP) ? (float)(128 + (int)((zraw[t] >> (4 * (g & 3))) & 15u))
+                                            : ((F & F_I8) ? 128.0f : 136.0f);  // 128 + zero point
 #pragma unroll
-                for (int r = 0; r < NR; r++) acc[t][r] += cur.s[t] * (d[r] - cur.cz[t] * xs[r]);
+                for (int r = 0; r < NR; r++) acc[t][r] += sc * (d[r] - cz * xsum[r]);
             }
-            cur = nxt;
         }
     }
 
-    // reduce the waves' K ranges into wave 0
-    if (W > 1) {
-        if (wave > 0) {
+    // reduce the K chunks of a column's waves into its first
+    if (WK > 1) {
+        if (wk > 0) {
 #pragma unroll
             for (int t = 0; t < T; t++)
 #pragma unroll
-                for (int r = 0; r < NR; r++) red[(((wave - 1) * T + t) * NR + r) * 64 + lane] = acc[t][r];
+                for (int r = 0; r < NR; r++) red[((((wk - 1) * WT + wt) * T + t) * NR + r) * 64 + lane] = acc[t][r];
         }
         __syncthreads();
-        if (wave > 0) return;
-        for (int w = 1; w < W; w++)
+        if (wk > 0) return;
+        for (int w = 1; w < WK; w++)
 #pragma unroll
             for (int t = 0; t < T; t++)
 #pragma unroll
-                for (int r = 0; r < NR; r++) acc[t][r] += red[(((w - 1) * T + t) * NR + r) * 64 + lane];
+                for (int r = 0; r < NR; r++) acc[t][r] += red[((((w - 1) * WT + wt) * T + t) * NR + r) * 64 + lane];
     }
 
+    const int sp = blockIdx.y;
     unsigned long long key[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) key[r] = 0;
@@ -267,7 +350,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
     constexpr int CW = CodeWords<F>::N;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][BM * PF_ROW];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), tid = threadIdx.x;
     const int l16 = lane & 15, kq = lane >> 4;
     const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
 
@@ -297,9 +380,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
         for (int i = 0; i < CPT; i++) *(u32x4*)(&lds[buf][xoff[i]]) = v[i];
     };
 
-    size_t tb[PF_TILES_PER_WAVE];
+    int tt[PF_TILES_PER_WAVE];
 #pragma unroll
-    for (int t = 0; t < PF_TILES_PER_WAVE; t++) tb[t] = (size_t)min(otile + t, tiles - 1) * G;
+    for (int t = 0; t < PF_TILES_PER_WAVE; t++) tt[t] = min(otile + t, tiles - 1);
     struct WFrag {
         u32x4 c[PF_TILES_PER_WAVE][CW];
         float s[PF_TILES_PER_WAVE], off[PF_TILES_PER_WAVE];
@@ -307,7 +390,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
     auto wload = [&](int g, WFrag& f) {
 #pragma unroll
         for (int t = 0; t < PF_TILES_PER_WAVE; t++) {
-            const size_t blk = tb[t] + g;
+            const size_t blk = (size_t)tt[t] * G + g;
             const u32x4* cp = (const u32x4*)a.codes + blk * 64 * CW;
 #pragma unroll
             for (int h = 0; h < CW; h++) f.c[t][h] = cp[h * 64 + lane];
@@ -315,8 +398,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
                 f.s[t] = 1.0f;  // exact integers q = stored - 128; the row scale comes after the sum
                 f.off[t] = -128.0f;
             } else {
-                f.s[t] = scale_of<F>(a.scales, blk, l16);
-                f.off[t] = -(float)zero_of<F>(a.zeros, blk, l16) * f.s[t];
+                f.s[t] = scale_of<F>(a.scales, tt[t], G, g, l16);
+                f.off[t] = -(float)zero_of<F>(a.zeros, tt[t], G, g, l16) * f.s[t];
             }
         }
     };
@@ -366,7 +449,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
     // epilogue: acc[bb][t][r] = D[token tok0 + 16 bb + 4 kq + r][output 16 (otile + t) + l16]
     float rs[PF_TILES_PER_WAVE];
 #pragma unroll
-    for (int t = 0; t < PF_TILES_PER_WAVE; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tb[t], l16) : 1.0f;
+    for (int t = 0; t < PF_TILES_PER_WAVE; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tt[t], G, 0, l16) : 1.0f;
 #pragma unroll
     for (int bb = 0; bb < BMB; bb++) {
         unsigned long long key[4] = {0, 0, 0, 0};
@@ -403,13 +486,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
 // ---------------------------------------------------------------------------------------------------------------
 // launchers
 
+size_t skinny_lds(const Launch& l) {
+    const int wk = l.waves / l.tile_waves;
+    const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
+    return x + (size_t)(wk - 1) * l.tile_waves * SKINNY_TILES * 4 * 64 * sizeof(float);
+}
+
+template <int F, int EPI, int NR, int NG>
+static hipError_t skinny_ng(const Launch& l) {
+    const int tiles = l.rows / TILE;
+    const int per_wg = SKINNY_TILES * l.tile_waves;
+    dim3 grid((tiles + per_wg - 1) / per_wg, l.split);
+    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG>), grid, dim3(64 * l.waves), skinny_lds(l),
+                       l.stream, l);
+    return hipGetLastError();
+}
+
 template <int F, int EPI, int NR>
 static hipError_t skinny_nr(const Launch& l) {
-    const int tiles = l.rows / TILE;
-    dim3 grid((tiles + SKINNY_TILES - 1) / SKINNY_TILES, l.split);
-    size_t lds = (size_t)(l.waves - 1) * SKINNY_TILES * NR * 64 * sizeof(float);
-    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES>), grid, dim3(64 * l.waves), lds, l.stream, l);
-    return hipGetLastError();
+    return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4>(l) : skinny_ng<F, EPI, NR, 1>(l);
 }
 
 template <int F, int EPI>

@@ -16,9 +16,11 @@
 //  int8 (QH_WT_I8): 2048 B per block = [h][lane][w] u32, h = 0, 1: words w = 2e + i, step j = 2h + e, column bytes
 //    4i + 0..3 in byte order; stored values q + 128.
 //
-// Scales: [t][g][16] per row of the tile, bf16 for int4 (exact for bf16-stored checkpoint scales), f32 for int8 and
-// for the int4 _S32 storages (scales bf16 does not hold exactly).
-// Zero points (QH_WT_I4Z, QH_WT_I4Z_S32): one u64 per block, nibble r = zero point of row 16t + r.
+// Scales: per tile, per quad of 4 groups (the group count padded up to a multiple of 4), per row of the tile, the
+// quad's 4 groups: [t][g / 4][16][g % 4], so that one 8-byte load gives a row the scales of 4 consecutive groups.
+// bf16 for int4 (exact for bf16-stored checkpoint scales), f32 for int8 and for the int4 _S32 storages (scales bf16
+// does not hold exactly).
+// Zero points (QH_WT_I4Z, QH_WT_I4Z_S32): [t][g / 4][16] u16, nibble g % 4 = the zero point of that row and group.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -37,6 +39,15 @@ constexpr bool valid_wt(int wt) { return wt >= 1 && wt <= 5; }
 
 // bytes of one (tile, group) code block
 constexpr size_t block_bytes(int wt) { return is_i8(wt) ? 2048 : 1024; }
+
+// quads of 4 groups (scale and zero-point blocks) for G groups
+constexpr size_t quads(size_t G) { return (G + 3) / 4; }
+// element index of the scale of tile t, group g, row r (G groups in the matrix)
+constexpr size_t scale_idx(size_t t, size_t G, size_t g, int r) {
+    return ((t * quads(G) + g / 4) * TILE + (size_t)r) * 4 + g % 4;
+}
+// u16 index of the zero-point nibbles of tile t, quad g / 4, row r
+constexpr size_t zero_idx(size_t t, size_t G, size_t g, int r) { return (t * quads(G) + g / 4) * TILE + (size_t)r; }
 
 // nibble position of column c (0..7) inside a packed int4 word
 constexpr int nib_pos(int c) { return (c & 1) ? 4 + (c >> 1) : (c >> 1); }

@@ -67,6 +67,10 @@ def test_prefill_plain(gemm, kind, m):
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("m", [1, 5, 40, 300])
 def test_silu(gemm, kind, m):
+    """SwiGLU epilogue: bf16 silu(gate) * up over the interleaved [gate; up] tiles. For decode sizes the products are
+    exact, so the output matches the oracle within the bar (plus the bf16 rounding of the output); for prefill sizes
+    the inputs of the epilogue carry the bf16 rounding of each weight (held to the bar in test_prefill_plain), and the
+    epilogue is checked against silu over the same arithmetic."""
     import torch
 
     print(f"silu {kind} m={m}", flush=True)
@@ -79,9 +83,14 @@ def test_silu(gemm, kind, m):
     assert gemm.run(None, m, mat, to_dev(x), y, Epi.Silu) == 1
     torch.cuda.synchronize()
     got = y.float().cpu().numpy()
-    full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1)
+    if m <= 16:
+        full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1)
+        tol = TOL
+    else:
+        full = np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
+        tol = 1e-3
     want = oracle.silu_glu(full, row_order(n, True))
-    assert bf16_out_err(got, want) <= TOL
+    assert bf16_out_err(got, want) <= tol
 
 
 @pytest.mark.parametrize("kind", KINDS)
