@@ -61,10 +61,11 @@ def test_errors_report():
 
 
 def test_sizes():
-    assert packed_sizes(Wt.I4, 32, 256) == (2 * 2 * 1024, 2 * 2 * 16 * 2, 0)
-    assert packed_sizes(Wt.I4Z, 32, 256) == (4096, 128, 32)
-    assert packed_sizes(Wt.I4Z_S32, 32, 256) == (4096, 256, 32)
-    assert packed_sizes(Wt.I8, 16, 128) == (2048, 64, 0)
+    # codes: 1 KiB (int4) / 2 KiB (int8) per 16 rows x 128 columns; scales and zero points by quads of 4 groups
+    assert packed_sizes(Wt.I4, 32, 256) == (2 * 2 * 1024, 2 * 1 * 16 * 4 * 2, 0)
+    assert packed_sizes(Wt.I4Z, 32, 256) == (4096, 256, 2 * 16 * 2)
+    assert packed_sizes(Wt.I4Z_S32, 32, 1024) == (2 * 8 * 1024, 2 * 2 * 16 * 4 * 4, 2 * 2 * 16 * 2)
+    assert packed_sizes(Wt.I8, 16, 128) == (2048, 16 * 4 * 4, 0)
 
 
 def test_gemm_rejects_null_without_gpu():
