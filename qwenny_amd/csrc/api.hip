@@ -16,9 +16,12 @@ using namespace qh;
 
 struct qh_ctx {
     int device;
+    // the argmax epilogue's scratch: table [ARGMAX_SPREAD][ARGMAX_MAX_TOK] u64, then the workgroup counter; zeroed
+    // here and left zero by every launch
+    void* argmax_scratch;
     int cus;             // compute units
     int skinny_max_w;       // skinny kernel: most waves per workgroup splitting K (non-plain epilogues)
-    int skinny_tile_waves;  // skinny kernel, plain products: waves per workgroup side by side over tiles
+    int skinny_tile_waves;  // skinny kernel, plain products: waves side by side over tiles (0: by token count)
 };
 
 static int env_int(const char* name, int dflt) {
@@ -54,12 +57,23 @@ extern "C" int qh_open(int device, qh_ctx** out) {
     int cus = 0;
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     // QH_SKINNY_MAX_W / QH_SKINNY_TILE_WAVES override the skinny partition (tuning sweeps)
-    *out = new qh_ctx{device, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
-                      std::min(16, std::max(1, env_int("QH_SKINNY_TILE_WAVES", 4)))};
+    void* scratch = nullptr;
+    const size_t scratch_bytes = ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8 + 256;
+    HIP_TRY(hipMalloc(&scratch, scratch_bytes));
+    if (hipMemset(scratch, 0, scratch_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(scratch);
+        return fail(QH_EHIP, "argmax scratch: clear failed");
+    }
+    *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
+                      std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0)))};
     return QH_OK;
 }
 
-extern "C" void qh_close(qh_ctx* ctx) { delete ctx; }
+extern "C" void qh_close(qh_ctx* ctx) {
+    if (!ctx) return;
+    if (ctx->argmax_scratch) (void)hipFree(ctx->argmax_scratch);
+    delete ctx;
+}
 
 static void mat_release(qh_mat* m) {
     if (!m) return;
@@ -212,26 +226,30 @@ struct Partition {
 };
 
 // The skinny kernel's partition of a product of m tokens (kernels.hip skinny_kernel): each wave takes SKINNY_TILES
-// tiles and 4 groups (1 when the group count is not a multiple of 4). Plain products: workgroups of 4 waves side by
-// side over tiles, the grid split over every chunk of K (split-K partials the consumer sums). Other epilogues need
-// whole sums in one workgroup: its waves split K (reduced through LDS), as many as divide the groups evenly and let
-// the super-chunk's activations fit in LDS; longer K is walked in super-chunks.
+// tiles and 4 groups (1 when the group count is not a multiple of 4); a workgroup stages the activations of its
+// super-chunk of K once for all its waves, so the more wave columns (tile_waves) share it, the less that costs
+// relative to the weights (m / (4 * tile_waves * SKINNY_TILES) of the int4 bytes).
+// Plain products: workgroups of wave columns side by side over tiles, the grid split over every chunk of K (split-K
+// partials the consumer sums). Other epilogues need whole sums in one workgroup: its wave rows split K (reduced
+// through LDS), as many as divide the chunks evenly and fit 16 waves and the LDS; longer K is walked in super-chunks.
 static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tokens, bool plain) {
     const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
     const int cols = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;  // wave columns over the tiles
     const int ng = G % 4 == 0 ? 4 : 1;
+    const int want_wt = ctx->skinny_tile_waves > 0 ? ctx->skinny_tile_waves : (tokens <= 2 ? 4 : 8);
     if (plain) {
-        const int wt = std::max(1, std::min(ctx->skinny_tile_waves, cols));
+        const int wt = std::max(1, std::min(want_wt, cols));
         return Partition{wt, wt, G / ng, ng};
     }
-    const size_t per_group = (size_t)std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's x
+    const size_t per_group = std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's activations
+    const int wt = std::max(1, std::min({tokens <= 2 ? 2 : 8, cols, ctx->skinny_max_w}));
     int wk = 1;
-    for (int w = std::min(ctx->skinny_max_w, G / ng); w >= 1; w--)
+    for (int w = std::min(ctx->skinny_max_w / wt, G / ng); w >= 1; w--)
         if ((G / ng) % w == 0 && (size_t)w * ng * per_group <= SKINNY_X_LDS) {
             wk = w;
             break;
         }
-    return Partition{1, wk, 1, ng};
+    return Partition{wt, wt * wk, 1, ng};
 }
 
 extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
@@ -261,6 +279,8 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
         return fail(QH_EINVAL, "x rows of %zu elements at %p: 16-byte aligned rows of at least %zu", ldx, x, w->cols);
     const size_t m = epi == QH_EPI_ARGMAX ? n_out : n;
     if (m == 0) return 1;
+    if (epi == QH_EPI_ARGMAX && m > (size_t)ARGMAX_MAX_TOK)
+        return fail(QH_EINVAL, "argmax over %zu logit rows: at most %d", m, ARGMAX_MAX_TOK);
     if (m > (1u << 24) || w->rows > (1u << 30) || ldx > (1u << 30)) return fail(QH_EINVAL, "gemm: sizes too large");
     Launch l{};
     l.codes = w->codes;
@@ -278,6 +298,8 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     l.y = y;
     l.ldy = (int)(epi == QH_EPI_SILU ? w->rows / 2 : w->rows);
     l.keys = (unsigned long long*)keys;
+    l.argmax_table = (unsigned long long*)ctx->argmax_scratch;
+    l.argmax_count = (unsigned*)((uint8_t*)ctx->argmax_scratch + ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8);
     l.epi = epi;
     l.stream = (hipStream_t)stream;
     l.bf16_magic = 0x43004300u;

@@ -29,6 +29,8 @@ struct Launch {
     void* y;
     int ldy;                // elements between y rows
     unsigned long long* keys;
+    unsigned long long* argmax_table;  // [ARGMAX_SPREAD][ARGMAX_MAX_TOK], zero between launches
+    unsigned* argmax_count;            // workgroups done, zero between launches
     int epi;                // enum qh_epi
     int split;              // grid split-K (plain products only)
     int waves;              // waves per workgroup (skinny kernel): tile_waves over tiles x waves / tile_waves over K
@@ -38,6 +40,11 @@ struct Launch {
     uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;
 };
+
+// The argmax epilogue's scratch table: rows the workgroups spread their maxima over, and the logit rows of a step
+// it takes at most (the reference's MAX_OUT).
+constexpr int ARGMAX_SPREAD = 64;
+constexpr int ARGMAX_MAX_TOK = 64;
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
 constexpr int SKINNY_MAX_M = 16;

@@ -108,6 +108,47 @@ __device__ __forceinline__ unsigned long long group16_max(unsigned long long k) 
     return k;
 }
 
+// The argmax across workgroups without every workgroup hitting the same cache line of keys[]: a workgroup folds its
+// per-token maxima into one of ARGMAX_SPREAD rows of a scratch table (row = its index mod ARGMAX_SPREAD), and the last
+// workgroup of the launch folds the table into keys[] (one atomicMax per token), zeroing it as it reads, and resets
+// the workgroup counter: the next launch (or graph replay) starts from a clean table. One launch at a time per
+// context uses the table (launches on one stream).
+//
+// Ordering uses device-scope atomics only, no release fences: a fence at device scope writes back the XCD's L2 on
+// this part, far too costly once per workgroup. Every table and counter update is a returning device-scope atomic
+// (performed at the device's coherence point); a workgroup waits for its own to return before it counts itself done,
+// and the last workgroup reads the table with atomic exchanges after its count returned.
+__device__ __forceinline__ void argmax_spread_max(const Launch& a, int tok, unsigned long long k) {
+    const int row = (blockIdx.y * gridDim.x + blockIdx.x) % ARGMAX_SPREAD;
+    (void)__hip_atomic_fetch_max(a.argmax_table + row * ARGMAX_MAX_TOK + tok, k, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ void argmax_finish(const Launch& a) {
+    __shared__ int last;
+    __shared__ unsigned long long best[ARGMAX_MAX_TOK];
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's table updates have returned
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.argmax_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x * gridDim.y - 1;
+    for (int t = threadIdx.x; t < a.m; t += blockDim.x) best[t] = 0;
+    __syncthreads();
+    if (!last) return;  // uniform over the workgroup
+    for (int i = threadIdx.x; i < ARGMAX_SPREAD * a.m; i += blockDim.x) {
+        const int row = i / a.m, tok = i - row * a.m;
+        const unsigned long long k = __hip_atomic_exchange(a.argmax_table + row * ARGMAX_MAX_TOK + tok, 0ull,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (k) atomicMax(best + tok, k);
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < a.m; t += blockDim.x)
+        if (best[t])
+            (void)__hip_atomic_fetch_max(a.keys + t, best[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0)
+        (void)__hip_atomic_exchange(a.argmax_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Words of a (tile, group) code block per lane (16 bytes each).
 template <int F>
 struct CodeWords {
@@ -281,7 +322,8 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
         }
     }
 
-    // reduce the K chunks of a column's waves into its first
+    // reduce the K chunks of a column's waves into its first (the others stay for the workgroup's barriers)
+    bool lead = true;
     if (WK > 1) {
         if (wk > 0) {
 #pragma unroll
@@ -290,33 +332,38 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
                 for (int r = 0; r < NR; r++) red[((((wk - 1) * WT + wt) * T + t) * NR + r) * 64 + lane] = acc[t][r];
         }
         __syncthreads();
-        if (wk > 0) return;
-        for (int w = 1; w < WK; w++)
+        lead = wk == 0;
+        if (lead)
+            for (int w = 1; w < WK; w++)
 #pragma unroll
-            for (int t = 0; t < T; t++)
+                for (int t = 0; t < T; t++)
 #pragma unroll
-                for (int r = 0; r < NR; r++) acc[t][r] += red[((((w - 1) * WT + wt) * T + t) * NR + r) * 64 + lane];
+                    for (int r = 0; r < NR; r++)
+                        acc[t][r] += red[((((w - 1) * WT + wt) * T + t) * NR + r) * 64 + lane];
     }
 
     const int sp = blockIdx.y;
     unsigned long long key[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) key[r] = 0;
+    if (lead) {
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-        const int tile = tile0 + t;
-        if (tile >= tiles) break;
-        const int out = tile * TILE + l16;
+        for (int t = 0; t < T; t++) {
+            const int tile = tile0 + t;
+            if (tile >= tiles) break;
+            const int out = tile * TILE + l16;
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const int tok = 4 * kq + r;
-            const float v = acc[t][r];
-            if (EPI == EPI_SILU) {
-                const float up = __shfl_xor(v, 8);
-                if (l16 < 8 && tok < M) ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(v) * up);
-            } else {
-                if (tok < M) ((float*)a.y)[((size_t)sp * M + tok) * a.ldy + out] = v;
-                if (EPI == EPI_ARGMAX && tok < M && out < a.valid) key[r] = max_u64(key[r], argmax_key(v, out));
+            for (int r = 0; r < NR; r++) {
+                const int tok = 4 * kq + r;
+                const float v = acc[t][r];
+                if (EPI == EPI_SILU) {
+                    const float up = __shfl_xor(v, 8);
+                    if (l16 < 8 && tok < M)
+                        ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(v) * up);
+                } else {
+                    if (tok < M) ((float*)a.y)[((size_t)sp * M + tok) * a.ldy + out] = v;
+                    if (EPI == EPI_ARGMAX && tok < M && out < a.valid) key[r] = max_u64(key[r], argmax_key(v, out));
+                }
             }
         }
     }
@@ -325,8 +372,9 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
         for (int r = 0; r < NR; r++) {
             const unsigned long long k = group16_max(key[r]);
             const int tok = 4 * kq + r;
-            if (l16 == 0 && tok < M && k) atomicMax(a.keys + tok, k);
+            if (lead && l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
         }
+        argmax_finish(a);
     }
 }
 
@@ -477,10 +525,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
             for (int r = 0; r < 4; r++) {
                 const unsigned long long k = group16_max(key[r]);
                 const int tok = tok0 + 16 * bb + 4 * kq + r;
-                if (l16 == 0 && tok < M && k) atomicMax(a.keys + tok, k);
+                if (l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
             }
         }
     }
+    if (EPI == EPI_ARGMAX) argmax_finish(a);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -123,3 +123,38 @@ def test_skinny_baseline_shape(gemm):
     x = activations(1, "x", 1, 2560)
     mat = Mat.stack(gemm, [q])
     assert rel_err(_plain(gemm, mat, x, 1), oracle_y(q, x)) <= 1e-4
+
+
+@pytest.mark.parametrize("n_out", [1, 5, 16, 64])
+def test_argmax_many_workgroups_repeated(gemm, n_out):
+    """Thousands of workgroups folding their maxima through the argmax scratch table, several launches in a row with
+    different activations: each launch's keys must be exactly those of its own logits (the table is left clean)."""
+    import torch
+
+    print(f"argmax many n_out={n_out}", flush=True)
+    n, k = 65536, 256
+    q = make_quant(43, "i4", n, k)
+    mat = Mat.stack(gemm, [q])
+    for rep in range(3):
+        x = activations(60 + rep, "x", n_out, k)
+        y = torch.zeros((n_out, n), dtype=torch.float32, device="cuda")
+        keys = torch.zeros(n_out, dtype=torch.int64, device="cuda")
+        gemm.run(None, n_out, mat, to_dev(x), y, Epi.Argmax, n_out=n_out, keys=keys)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert (keys.cpu().numpy().view(np.uint64) == oracle.argmax_keys(got, n)).all(), rep
+        assert rel_err(got, oracle_y(q, x)) <= TOL
+
+
+def test_argmax_rejects_too_many_rows(gemm):
+    import torch
+
+    from qwenny_amd._lib import QhError
+
+    q = make_quant(44, "i4", 64, 128)
+    mat = Mat.stack(gemm, [q])
+    x = to_dev(activations(1, "x", 65, 128))
+    y = torch.zeros((65, 64), dtype=torch.float32, device="cuda")
+    keys = torch.zeros(65, dtype=torch.int64, device="cuda")
+    with pytest.raises(QhError):
+        gemm.run(None, 65, mat, x, y, Epi.Argmax, n_out=65, keys=keys)
