@@ -22,6 +22,7 @@ struct qh_ctx {
     int cus;             // compute units
     int skinny_max_w;       // skinny kernel: most waves per workgroup splitting K (non-plain epilogues)
     int skinny_tile_waves;  // skinny kernel, plain products: waves side by side over tiles (0: by token count)
+    int pf_shape;           // prefill workgroup shape (0: by tail waste; QH_PF_SHAPE for tuning sweeps)
 };
 
 static int env_int(const char* name, int dflt) {
@@ -65,7 +66,8 @@ extern "C" int qh_open(int device, qh_ctx** out) {
         return fail(QH_EHIP, "argmax scratch: clear failed");
     }
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
-                      std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0)))};
+                      std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
+                      std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0)))};
     return QH_OK;
 }
 
@@ -303,6 +305,8 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     l.epi = epi;
     l.stream = (hipStream_t)stream;
     l.bf16_magic = 0x43004300u;
+    l.cus = ctx->cus;
+    l.pf_shape = ctx->pf_shape;
     l.nib_mask = 0x000F000Fu;
     if (m <= (size_t)SKINNY_MAX_M) {
         Partition p = skinny_partition(ctx, w, m, epi == QH_EPI_PLAIN && !whole);

@@ -36,6 +36,8 @@ struct Launch {
     int waves;              // waves per workgroup (skinny kernel): tile_waves over tiles x waves / tile_waves over K
     int tile_waves;
     int groups_per_wave;    // skinny kernel: 4, or 1 when the group count is not a multiple of 4
+    int cus;                // compute units (the prefill shape choice)
+    int pf_shape;           // prefill workgroup shape: 0 chosen by size, else forced (kernels.hip prefill_epi)
     uint32_t bf16_magic;    // 0x43004300: the bf16 pair (128, 128) (see kernels.hip i4_biased)
     uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;

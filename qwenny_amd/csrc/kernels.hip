@@ -12,10 +12,10 @@
 // by the wave's tiles). K is split over the waves of a workgroup (reduced through LDS) and, for plain products, over
 // the grid (the split-K partials of the output contract).
 //
-// prefill_kernel (m > 16): MFMA-bound. A workgroup of 4 waves computes 16 * BMB tokens x 128 outputs; the activation
-// tile goes through double-buffered, XOR-swizzled LDS in 64-column stages, each wave dequantizes its own 32 outputs'
-// weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), and the workgroups are
-// mapped XCD-aware so that those sharing a weight tile run on one XCD's L2.
+// prefill_kernel (m > 16): MFMA-bound. A workgroup of 8 waves computes up to 256 tokens x 256 outputs; the
+// activation tile goes through double-buffered, XOR-swizzled LDS in 64-column stages, each wave dequantizes its own
+// outputs' weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), and the
+// workgroups are mapped XCD-aware so that those sharing a weight tile run on one XCD's L2.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -64,6 +64,10 @@ __device__ __forceinline__ bf16x8 i8_biased(uint32_t a, uint32_t b) {
 // int4 word -> bf16 of (q - z) s = q s + off, in f32 then rounded once
 __device__ __forceinline__ bf16x8 i4_scaled(uint32_t w, float s, float off) {
     uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    // opaque to the optimizer: otherwise it folds the nibble mask into each byte extraction and loses the one-op
+    // byte-to-float conversions (v_cvt_f32_ubyte0..3)
+    asm("" : "+v"(lo));
+    asm("" : "+v"(hi));
     bf16x8 r;
     r[0] = (__bf16)__builtin_fmaf(byte_f(lo, 0), s, off);
     r[1] = (__bf16)__builtin_fmaf(byte_f(lo, 2), s, off);
@@ -380,26 +384,49 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // prefill_kernel
+//
+// On v_mfma_f32_32x32x16_bf16 (on gfx950 it sustains about twice the rate of the 16x16x32 form). A: 32 tokens x 16
+// columns of activations, lane l holding token l % 32, columns 8 (l / 32) .. + 7; B: 16 columns x 32 outputs (two
+// tiles), lane l holding output l % 32, the same columns; D: lane l holds output l % 32 of tokens
+// 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15.
+//
+// The same packed blocks as the skinny kernel serve as B: for a 32-output block (tiles 2p, 2p + 1) and a group, lane
+// l reads two 16-byte pieces of its tile's block, those of block lanes 16 (l / 32) + l % 16 and 32 + the same, which
+// hold its output row's columns for k16 steps 2i (first piece, word i) and 2i + 1 (second piece, word i).
+//
+// A workgroup of WM x WN waves computes WM * BMB * 32 tokens x WN * TN * 32 outputs; wave (wm, wn) owns BMB token
+// blocks x TN output blocks (BMB * TN accumulators of 16 registers). Activations go through double-buffered,
+// XOR-swizzled LDS in stages of 64 columns; each wave dequantizes its outputs' weights straight from global memory into
+// bf16 registers ((q - z) s in f32, rounded once). Workgroups are ordered XCD-aware, token tiles fastest, so that
+// those sharing a weight tile share an XCD's L2.
 
-constexpr int PF_WAVES = 4;
-constexpr int PF_TILES_PER_WAVE = 2;
-constexpr int PF_TILES = PF_WAVES * PF_TILES_PER_WAVE;  // 128 outputs per workgroup
-constexpr int PF_BK = 64;                               // columns per LDS stage (half a group)
-constexpr int PF_ROW = PF_BK * 2;                       // LDS bytes per token row of a stage
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// LDS byte offset of 16-byte chunk kc (0..7) of token row `row` in a stage: XOR-swizzled so that the 16 lanes of a
-// row group (16 tokens, one chunk) hit all 64 banks once.
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+}
+
+constexpr int PF_BK = 64;          // columns per LDS stage (half a group)
+constexpr int PF_ROW = PF_BK * 2;  // LDS bytes per token row of a stage
+
+// LDS byte offset of 16-byte chunk kc (0..7) of token row `row` in a stage: XOR-swizzled so that 16 lanes reading
+// 16 consecutive rows at one chunk hit all 64 banks once.
 __device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW + 16 * (kc ^ ((row >> 1) & 7)); }
 
-template <int F, int EPI, int BMB>
-__global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
-    constexpr int BM = 16 * BMB;
-    constexpr int CPT = BM * (PF_ROW / 16) / 256;  // 16-byte x chunks each thread stages per stage
+template <int F, int EPI, int BMB, int TN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
+    constexpr int NTHR = WM * WN * 64;
+    constexpr int BM = WM * BMB * 32;                // tokens per workgroup
+    constexpr int WTILES = WN * TN * 2;              // 16-row tiles per workgroup
+    constexpr int CPT = BM * (PF_ROW / 16) / NTHR;   // 16-byte x pieces each thread stages per stage
+    static_assert(CPT >= 1 && CPT * NTHR == BM * (PF_ROW / 16), "stage pieces must divide over the threads");
     constexpr int CW = CodeWords<F>::N;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][BM * PF_ROW];
+    constexpr int STAGE = BM * PF_ROW;               // LDS bytes of one stage
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), tid = threadIdx.x;
-    const int l16 = lane & 15, kq = lane >> 4;
+    const int wm = wave % WM, wn = wave / WM;
+    const int l32 = lane & 31, lh = lane >> 5, l16 = lane & 15;
     const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
 
     // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous run of work items, token tiles
@@ -407,129 +434,181 @@ __global__ __launch_bounds__(256) void prefill_kernel(Launch a) {
     const int nb = gridDim.x, b = blockIdx.x, xcd = b & 7, q8 = nb >> 3, r8 = nb & 7;
     const int item = xcd * q8 + min(xcd, r8) + (b >> 3);
     const int ntok = (M + BM - 1) / BM;
-    const int tok0 = (item % ntok) * BM, otile = (item / ntok) * PF_TILES + wave * PF_TILES_PER_WAVE;
+    const int tok0 = (item % ntok) * BM;
+    const int tile0 = (item / ntok) * WTILES + wn * TN * 2;  // the wave's first tile
+    const int wtok0 = wm * BMB * 32;                         // the wave's first token row in the stage
 
-    // staging of the activation tile: chunk c = tid + 256 i -> row c / 8, column chunk c % 8
-    const __bf16* xsrc[CPT];
-    int xoff[CPT];
+    // Global loads take a wave-uniform base plus a 32-bit per-lane byte offset fixed for the whole kernel (no 64-bit
+    // address arithmetic per load). Activations: piece c = tid + NTHR i -> row c / 8, column chunk c % 8.
+    const uint8_t* xbase = (const uint8_t*)a.x;
+    uint32_t xg[CPT];
+    int xs[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
-        const int c = tid + 256 * i, row = c >> 3, kc = c & 7;
+        const int c = tid + NTHR * i, row = c >> 3, kc = c & 7;
         const int tok = min(tok0 + row, M - 1);
-        xsrc[i] = (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc;
-        xoff[i] = pf_lds_off(row, kc);
+        xg[i] = (uint32_t)(((size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc) * 2);
+        xs[i] = pf_lds_off(row, kc);
     }
     auto stage_load = [&](int s, u32x4 (&v)[CPT]) {
+        const uint8_t* p = xbase + (size_t)s * PF_ROW;
 #pragma unroll
-        for (int i = 0; i < CPT; i++) v[i] = *(const u32x4*)(xsrc[i] + (size_t)s * PF_BK);
+        for (int i = 0; i < CPT; i++) v[i] = *(const u32x4*)(p + xg[i]);
     };
     auto stage_store = [&](int buf, const u32x4 (&v)[CPT]) {
 #pragma unroll
-        for (int i = 0; i < CPT; i++) *(u32x4*)(&lds[buf][xoff[i]]) = v[i];
+        for (int i = 0; i < CPT; i++) *(u32x4*)(lds + buf * STAGE + xs[i]) = v[i];
     };
-
-    int tt[PF_TILES_PER_WAVE];
+    // LDS reads of A fragments: row wtok0 + 32 bb + l32, chunk 2 s16 + lh; the swizzle of rows 32 bb + l32 depends on
+    // l32 only, so the per-lane part is 4 offsets and the token block is an immediate
+    int xr[4];
 #pragma unroll
-    for (int t = 0; t < PF_TILES_PER_WAVE; t++) tt[t] = min(otile + t, tiles - 1);
+    for (int s16 = 0; s16 < 4; s16++) xr[s16] = pf_lds_off(wtok0 + l32, 2 * s16 + lh);
+
+    // this lane's output row: tile tt[t] (of output block t), row l16; its code pieces and scales as offsets
+    int tt[TN];
+    uint32_t cg[TN], sg[TN], zg[TN];
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        tt[t] = min(tile0 + 2 * t + (l32 >> 4), tiles - 1);
+        cg[t] = (uint32_t)(((size_t)tt[t] * G * 64 * CW + 16 * lh + l16) * 16);
+        sg[t] = (uint32_t)(scale_idx(tt[t], G, 0, l16) * ((F & F_S32) ? 4 : 2));
+        zg[t] = (uint32_t)(zero_idx(tt[t], G, 0, l16) * 2);
+    }
     struct WFrag {
-        u32x4 c[PF_TILES_PER_WAVE][CW];
-        float s[PF_TILES_PER_WAVE], off[PF_TILES_PER_WAVE];
+        u32x4 c[TN][2][CW];  // per output block: the two pieces (x CW words for int8)
+        float s[TN], off[TN];
     };
     auto wload = [&](int g, WFrag& f) {
+        const uint8_t* cb = (const uint8_t*)a.codes + (size_t)g * 64 * CW * 16;
+        const size_t sq = ((size_t)(g >> 2) * TILE * 4 + (g & 3)) * ((F & F_S32) ? 4 : 2);
 #pragma unroll
-        for (int t = 0; t < PF_TILES_PER_WAVE; t++) {
-            const size_t blk = (size_t)tt[t] * G + g;
-            const u32x4* cp = (const u32x4*)a.codes + blk * 64 * CW;
+        for (int t = 0; t < TN; t++) {
 #pragma unroll
-            for (int h = 0; h < CW; h++) f.c[t][h] = cp[h * 64 + lane];
+            for (int pc = 0; pc < 2; pc++)
+#pragma unroll
+                for (int h = 0; h < CW; h++) f.c[t][pc][h] = *(const u32x4*)(cb + cg[t] + (h * 64 + 32 * pc) * 16);
             if (F & F_PERCH) {
                 f.s[t] = 1.0f;  // exact integers q = stored - 128; the row scale comes after the sum
                 f.off[t] = -128.0f;
             } else {
-                f.s[t] = scale_of<F>(a.scales, tt[t], G, g, l16);
-                f.off[t] = -(float)zero_of<F>(a.zeros, tt[t], G, g, l16) * f.s[t];
+                const uint8_t* sp = (const uint8_t*)a.scales + sq + sg[t];
+                f.s[t] = (F & F_S32) ? *(const float*)sp : bf16_bits_f(*(const uint16_t*)sp);
+                int z = (F & F_I8) ? 128 : 8;
+                if (F & F_ZP)
+                    z = (*(const uint16_t*)((const uint8_t*)a.zeros + (size_t)(g >> 2) * TILE * 2 + zg[t]) >>
+                         (4 * (g & 3))) & 15;
+                f.off[t] = -(float)z * f.s[t];
             }
         }
     };
+    // B fragment of output block t for k16 step kk (0..7) of the group
+    auto dequant = [&](const WFrag& f, int t, int kk) -> bf16x8 {
+        const int pc = kk & 1, i = kk >> 1;
+        if (F & F_I8)  // int8: word pair (2e, 2e + 1) of half h, for k32 step i = 2h + e
+            return i8_scaled(f.c[t][pc][i >> 1][2 * (i & 1)], f.c[t][pc][i >> 1][2 * (i & 1) + 1], f.s[t], f.off[t]);
+        return i4_scaled(f.c[t][pc][0][i], f.s[t], f.off[t]);
+    };
 
-    f32x4 acc[BMB][PF_TILES_PER_WAVE];
+    f32x16 acc[BMB][TN];
 #pragma unroll
     for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
-        for (int t = 0; t < PF_TILES_PER_WAVE; t++) acc[bb][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < TN; t++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[bb][t][e] = 0.0f;
 
-    const int stages = 2 * G;
+    // one stage (64 columns, half hh of the group) from LDS buffer `buf`: the A fragments of k16 step s16 + 1 are read
+    // while step s16's MFMAs run
+    auto compute = [&](int buf, int hh, const WFrag& w) {
+        const uint8_t* lb = lds + buf * STAGE;
+        u32x4 xa[2][BMB];
+#pragma unroll
+        for (int bb = 0; bb < BMB; bb++) xa[0][bb] = *(const u32x4*)(lb + xr[0] + bb * 32 * PF_ROW);
+#pragma unroll
+        for (int s16 = 0; s16 < 4; s16++) {
+            if (s16 < 3) {
+#pragma unroll
+                for (int bb = 0; bb < BMB; bb++)
+                    xa[(s16 + 1) & 1][bb] = *(const u32x4*)(lb + xr[s16 + 1] + bb * 32 * PF_ROW);
+            }
+            bf16x8 bw[TN];
+#pragma unroll
+            for (int t = 0; t < TN; t++) bw[t] = dequant(w, t, 4 * hh + s16);
+#pragma unroll
+            for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+                for (int t = 0; t < TN; t++) acc[bb][t] = mfma32(xa[s16 & 1][bb], bw[t], acc[bb][t]);
+        }
+    };
+
+    // group g: stage 2g from buffer 0 while stage 2g + 1 is loaded, then stage 2g + 1 from buffer 1 while stage
+    // 2g + 2 is loaded; the next group's weights are loaded one group ahead
     u32x4 xv[CPT];
     WFrag wcur, wnxt;
     stage_load(0, xv);
     wload(0, wcur);
     stage_store(0, xv);
     __syncthreads();
-    for (int s = 0; s < stages; s++) {
-        const bool more = s + 1 < stages;
-        if (more) stage_load(s + 1, xv);
-        if (s & 1) wload(min(s / 2 + 1, G - 1), wnxt);
-        const uint8_t* buf = lds[s & 1];
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-            const int j = 2 * (s & 1) + jj;  // k32 step within the group
-            bf16x8 bw[PF_TILES_PER_WAVE];
-#pragma unroll
-            for (int t = 0; t < PF_TILES_PER_WAVE; t++) {
-                if (F & F_I8)
-                    bw[t] = i8_scaled(wcur.c[t][j >> 1][2 * (j & 1)], wcur.c[t][j >> 1][2 * (j & 1) + 1], wcur.s[t],
-                                      wcur.off[t]);
-                else
-                    bw[t] = i4_scaled(wcur.c[t][0][j], wcur.s[t], wcur.off[t]);
-            }
-#pragma unroll
-            for (int bb = 0; bb < BMB; bb++) {
-                const u32x4 xa = *(const u32x4*)(buf + pf_lds_off(16 * bb + l16, 4 * jj + kq));
-#pragma unroll
-                for (int t = 0; t < PF_TILES_PER_WAVE; t++) acc[bb][t] = mfma(xa, bw[t], acc[bb][t]);
-            }
-        }
-        if (more) stage_store((s + 1) & 1, xv);
+    for (int g = 0; g < G; g++) {
+        const bool more = g + 1 < G;
+        stage_load(2 * g + 1, xv);
+        wload(more ? g + 1 : g, wnxt);
+        compute(0, 0, wcur);
+        stage_store(1, xv);
         __syncthreads();
-        if (s & 1) wcur = wnxt;
+        if (more) stage_load(2 * g + 2, xv);
+        compute(1, 1, wcur);
+        if (more) stage_store(0, xv);
+        __syncthreads();
+        wcur = wnxt;
     }
 
-    // epilogue: acc[bb][t][r] = D[token tok0 + 16 bb + 4 kq + r][output 16 (otile + t) + l16]
-    float rs[PF_TILES_PER_WAVE];
+    // epilogue: acc[bb][t][v] = D[token tok0 + wtok0 + 32 bb + 8 (v / 4) + 4 lh + v % 4][output 32-block t, l32]
+    float rs[TN];
 #pragma unroll
-    for (int t = 0; t < PF_TILES_PER_WAVE; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tt[t], G, 0, l16) : 1.0f;
+    for (int t = 0; t < TN; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tt[t], G, 0, l16) : 1.0f;
+    unsigned long long key[BMB][16];
 #pragma unroll
-    for (int bb = 0; bb < BMB; bb++) {
-        unsigned long long key[4] = {0, 0, 0, 0};
+    for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
-        for (int t = 0; t < PF_TILES_PER_WAVE; t++) {
-            const int tile = otile + t;
-            if (tile >= tiles) break;
-            const int out = tile * TILE + l16;
+        for (int v = 0; v < 16; v++) key[bb][v] = 0;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int tok = tok0 + 16 * bb + 4 * kq + r;
-                const float v = (F & F_PERCH) ? acc[bb][t][r] * rs[t] : acc[bb][t][r];
+    for (int t = 0; t < TN; t++) {
+        const int tile = tile0 + 2 * t + (l32 >> 4);
+        const bool tile_ok = tile < tiles;
+        const int out = tile * TILE + l16;
+#pragma unroll
+        for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
+                const float val = (F & F_PERCH) ? acc[bb][t][v] * rs[t] : acc[bb][t][v];
                 if (EPI == EPI_SILU) {
-                    const float up = __shfl_xor(v, 8);
-                    if (l16 < 8 && tok < M)
-                        ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(v) * up);
+                    const float up = __shfl_xor(val, 8);
+                    if (tile_ok && l16 < 8 && tok < M)
+                        ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(val) * up);
                 } else {
-                    if (tok < M) ((float*)a.y)[(size_t)tok * a.ldy + out] = v;
-                    if (EPI == EPI_ARGMAX && tok < M && out < a.valid) key[r] = max_u64(key[r], argmax_key(v, out));
+                    if (tile_ok && tok < M) ((float*)a.y)[(size_t)tok * a.ldy + out] = val;
+                    if (EPI == EPI_ARGMAX && tile_ok && tok < M && out < a.valid)
+                        key[bb][v] = max_u64(key[bb][v], argmax_key(val, out));
                 }
             }
-        }
-        if (EPI == EPI_ARGMAX) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const unsigned long long k = group16_max(key[r]);
-                const int tok = tok0 + 16 * bb + 4 * kq + r;
-                if (l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
-            }
-        }
     }
-    if (EPI == EPI_ARGMAX) argmax_finish(a);
+    if (EPI == EPI_ARGMAX) {
+        // the max over the 32 lanes that share a token (one lane half)
+#pragma unroll
+        for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                unsigned long long k = key[bb][v];
+#pragma unroll
+                for (int o = 1; o < 32; o <<= 1) k = max_u64(k, __shfl_xor(k, o));
+                const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (l32 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
+            }
+        argmax_finish(a);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -566,18 +645,45 @@ static hipError_t skinny_epi(const Launch& l) {
     }
 }
 
-template <int F, int EPI, int BMB>
-static hipError_t prefill_bm(const Launch& l) {
+template <int F, int EPI, int BMB, int TN, int WM, int WN>
+static hipError_t prefill_cfg(const Launch& l) {
     const int tiles = l.rows / TILE;
-    const int items = ((tiles + PF_TILES - 1) / PF_TILES) * ((l.m + 16 * BMB - 1) / (16 * BMB));
-    hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB>), dim3(items), dim3(256), 0, l.stream, l);
+    const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32;
+    const int items = ((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
+    hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN>), dim3(items), dim3(WM * WN * 64), 0, l.stream, l);
     return hipGetLastError();
+}
+
+// The prefill workgroup shape (tokens x outputs; waves): the largest tile that still makes two waves per CU
+// (256 x 256 on 8 waves of 256 x 32, then 256 x 128 and 128 x 128 on 4 waves), 64 x 128 for the smallest steps;
+// QH_PF_SHAPE forces one in tuning sweeps.
+template <int F, int EPI>
+static hipError_t prefill_epi(const Launch& l) {
+    const int tiles = l.rows / TILE;
+    auto items = [&](int bm, int wg_tiles) {
+        return (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
+    };
+    int shape = l.pf_shape;
+    if (shape == 0) {  // enough waves: at least two per CU
+        if (l.m > 128 && items(256, 16) * 8 >= 2 * l.cus) shape = 2;
+        else if (l.m > 128 && items(256, 8) * 4 >= 2 * l.cus) shape = 1;
+        else if (l.m > 64 && items(128, 8) * 4 >= 2 * l.cus) shape = 5;
+        else shape = 6;
+    }
+    switch (shape) {
+        case 1: return prefill_cfg<F, EPI, 8, 1, 1, 4>(l);   // 256 x 128; 4 waves of 256 x 32
+        case 2: return prefill_cfg<F, EPI, 8, 1, 1, 8>(l);   // 256 x 256; 8 waves of 256 x 32
+        case 3: return prefill_cfg<F, EPI, 4, 2, 2, 4>(l);   // 256 x 256; 8 waves of 128 x 64
+        case 4: return prefill_cfg<F, EPI, 8, 2, 1, 4>(l);   // 256 x 256; 4 waves of 256 x 64
+        case 5: return prefill_cfg<F, EPI, 4, 1, 1, 4>(l);   // 128 x 128; 4 waves of 128 x 32
+        default: return prefill_cfg<F, EPI, 2, 1, 1, 4>(l);  // 64 x 128; 4 waves of 64 x 32
+    }
 }
 
 template <int F, int EPI>
 static hipError_t launch_epi(const Launch& l) {
     if (l.m <= SKINNY_MAX_M) return skinny_epi<F & ~F_PERCH, EPI>(l);
-    return l.m > 128 ? prefill_bm<F, EPI, 16>(l) : prefill_bm<F, EPI, 4>(l);
+    return prefill_epi<F, EPI>(l);
 }
 
 template <int F>
