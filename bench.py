@@ -101,32 +101,38 @@ class Step:
         return sum(f for *_, f in self.launches)
 
 
-def time_step(step, steps, warmup, graph=True):
-    """ms per step over `steps` replays, HIP events on the launching stream, after `warmup` replays."""
+def time_step(step, steps, warmup, graph=True, per_graph=10):
+    """ms per step over `steps` steps, HIP events on the launching stream, after `warmup` steps. With `graph`, the
+    step's launches are captured `per_graph` times into one HIP graph (so that the replay's own start-up, about
+    20 us, is spread over that many steps) and the graph is replayed steps / per_graph times."""
     import torch
 
     stream = torch.cuda.current_stream()
-    g = None
     if graph:
+        per_graph = max(1, min(per_graph, steps))
         step.run()  # the kernels' first launches outside the capture
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
         with torch.cuda.stream(s):
             with torch.cuda.graph(g, stream=s):
-                step.run(s)
+                for _ in range(per_graph):
+                    step.run(s)
         torch.cuda.synchronize()
-    go = g.replay if g is not None else step.run
-    for _ in range(warmup):
+        go, reps = g.replay, max(1, steps // per_graph)
+        warm = max(1, warmup // per_graph)
+    else:
+        go, reps, warm, per_graph = step.run, steps, warmup, 1
+    for _ in range(warm):
         go()
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for _ in range(steps):
+    for _ in range(reps):
         go()
     t1.record(stream)
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    return t0.elapsed_time(t1) / (reps * per_graph)
 
 
 def cpu_baseline(budget_s=12.0):
@@ -152,6 +158,10 @@ def cpu_baseline(budget_s=12.0):
                       f"scalar C restatement of Quant::row_into + f32 dot, {threads} threads, {el:.1f} s"}
 
 
+TRAFFIC_NAME = "skinny_i4_m1_27b_set"
+COPY_BYTES = 512 << 20  # the calibration copy: reads and writes this many bytes
+
+
 def load_traffic(name):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if there is one for this workload."""
     p = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
@@ -159,6 +169,65 @@ def load_traffic(name):
         with open(p) as f:
             return json.load(f).get("traffic_bytes_per_launch")
     return None
+
+
+def traffic_run(gemm, set_mats, steps=5):
+    """The workload of the rocprofv3 --pmc passes: the roofline kernel's launches (27B set at M=1, plain, no graph)
+    and a plain torch copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES) that calibrates the counters."""
+    import torch
+
+    from qwenny_amd import Epi
+
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    st = Step(gemm, 1, 17408)
+    for c in range(4):
+        for mats, (k, n) in zip(set_mats, SET_27B):
+            st.add(mats[c], Epi.Plain, int4_bytes(k, n, 1), 2 * k * n)
+    for _ in range(steps):
+        st.run()
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_run": "done", "launches": steps * len(st.launches), "algorithmic_bytes_per_launch":
+                      st.bytes() / len(st.launches)}))
+
+
+def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
+    """From the two rocprofv3 --pmc CSVs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch): the copy kernel's readings
+    give the scale factors (known bytes / reading), the skinny kernel's mean readings scaled by them give its HBM bytes
+    per launch. Writes profiles/<out_name>_traffic.json."""
+    import csv
+    import glob
+
+    def readings(d, counter):
+        out = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                name = r["Kernel_Name"]
+                kind = "copy" if ("copy" in name.lower() and "skinny" not in name) else (
+                    "skinny" if "skinny_kernel" in name else None)
+                if kind:
+                    out.setdefault(kind, []).append(float(r["Counter_Value"]))
+        return out
+
+    fetch, write = readings(fetch_dir, "FETCH_SIZE"), readings(write_dir, "WRITE_SIZE")
+    mean = lambda v: sum(v) / len(v)
+    # the copy: the largest readings are the full copies (torch may launch small copies too)
+    fcopy, wcopy = max(fetch["copy"]), max(write["copy"])
+    ffac, wfac = COPY_BYTES / (fcopy * 1024), COPY_BYTES / (wcopy * 1024)
+    fk, wk = mean(fetch["skinny"]) * 1024 * ffac, mean(write["skinny"]) * 1024 * wfac
+    res = {"kernel": "skinny_kernel int4 M=1, 27B layer set (5 shapes x 4 copies)",
+           "fetch_kib_per_dispatch": mean(fetch["skinny"]), "write_kib_per_dispatch": mean(write["skinny"]),
+           "copy_fetch_kib": fcopy, "copy_write_kib": wcopy, "copy_bytes": COPY_BYTES,
+           "fetch_scale": ffac, "write_scale": wfac, "traffic_bytes_per_launch": round(fk + wk),
+           "fetch_bytes_per_launch": round(fk), "write_bytes_per_launch": round(wk)}
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, "profiles", f"{out_name}_traffic.json"), "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res))
 
 
 def main():
@@ -169,7 +238,13 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8")
+    ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/*_traffic.json from the two --pmc runs' output directories")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: the products run on one MI355X; --gpus must be 1 "
                                    "(how they would shard is described in DESIGN.md)"}))
@@ -184,6 +259,9 @@ def main():
     only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
+    if args.traffic_run:
+        traffic_run(gemm, set_mats)
+        return
     head = upload_copies(gemm, quant(200, "i4", *HEAD_27B), 1)[0]
 
     def decode_step(m):
@@ -202,6 +280,18 @@ def main():
     out["m1"] = {"ms_per_step": ms, "GB/s": gbs, "launches": launches, "bytes": step.bytes()}
     print(f"# M=1 27B set x4 + head: {ms:.4f} ms/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK:.1%} of 8 TB/s)",
           file=sys.stderr, flush=True)
+
+    # the roofline kernel alone: the set's plain skinny launches (one kernel: rocprof's average duration for it is
+    # the same quantity)
+    rst = Step(gemm, 1, 17408)
+    for c in range(4):
+        for mats, (k, n) in zip(set_mats, SET_27B):
+            rst.add(mats[c], Epi.Plain, int4_bytes(k, n, 1), 2 * k * n)
+    rms = time_step(rst, args.steps, args.warmup, not args.no_graph)
+    per_launch_bytes = rst.bytes() / len(rst.launches)
+    per_launch_s = rms * 1e-3 / len(rst.launches)
+    print(f"# roofline kernel (plain M=1 set): {per_launch_s * 1e6:.2f} us per launch, "
+          f"{per_launch_bytes / per_launch_s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 
     extra = {}
     if "m5" in only:
@@ -232,8 +322,6 @@ def main():
         extra["int8_m1_GBps"] = round(st.bytes() / (ms8 * 1e-3) / 1e9, 1)
         print(f"# int8 M=1: {ms8:.4f} ms/step, {extra['int8_m1_GBps']} GB/s", file=sys.stderr, flush=True)
 
-    per_launch_bytes = step.bytes() / launches
-    per_launch_s = ms * 1e-3 / launches
     line = {
         "metric": "int4 GEMM HBM GB/s (% of 8 TB/s) at M=1/5; TFLOP/s (% bf16 MFMA peak) at M=2048",
         "value": round(gbs, 1),
@@ -252,9 +340,9 @@ def main():
                    "m": 1, "copies": 4, "graph": not args.no_graph},
         "roofline": {"bound": "hbm", "achieved": round(per_launch_bytes / per_launch_s / 1e9, 1), "peak": HBM_PEAK,
                      "unit": "GB/s", "frac": round(per_launch_bytes / per_launch_s / 1e9 / HBM_PEAK, 4),
-                     "traffic": load_traffic("skinny_i4_m1_27b"),
-                     "kernel": "skinny_kernel (int4, M=1)", "bytes_per_launch": round(per_launch_bytes),
-                     "launches_per_step": launches},
+                     "traffic": load_traffic(TRAFFIC_NAME),
+                     "kernel": "skinny_kernel<int4, plain, M=1> over the 27B set (20 launches)",
+                     "bytes_per_launch": round(per_launch_bytes), "us_per_launch": round(per_launch_s * 1e6, 3)},
         "extra": extra,
     }
     if not args.no_cpu:
