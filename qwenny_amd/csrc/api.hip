@@ -20,7 +20,8 @@ struct qh_ctx {
     // here and left zero by every launch
     void* argmax_scratch;
     int cus;             // compute units
-    int skinny_max_w;       // skinny kernel: most waves per workgroup splitting K (non-plain epilogues)
+    int skinny_max_w;       // skinny kernel: most waves per workgroup (non-plain epilogues)
+    int skinny_fill;        // skinny kernel, non-plain epilogues: waves per CU a launch aims for
     int skinny_tile_waves;  // skinny kernel, plain products: waves side by side over tiles (0: by token count)
     int pf_shape;           // prefill workgroup shape (0: by tail waste; QH_PF_SHAPE for tuning sweeps)
 };
@@ -66,6 +67,7 @@ extern "C" int qh_open(int device, qh_ctx** out) {
         return fail(QH_EHIP, "argmax scratch: clear failed");
     }
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
+                      std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
                       std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0)))};
     return QH_OK;
@@ -233,7 +235,8 @@ struct Partition {
 // relative to the weights (m / (4 * tile_waves * SKINNY_TILES) of the int4 bytes).
 // Plain products: workgroups of wave columns side by side over tiles, the grid split over every chunk of K (split-K
 // partials the consumer sums). Other epilogues need whole sums in one workgroup: its wave rows split K (reduced
-// through LDS), as many as divide the chunks evenly and fit 16 waves and the LDS; longer K is walked in super-chunks.
+// through LDS), as few as give the launch enough waves to fill the CUs, dividing the chunks evenly and fitting the wave
+// and LDS limits; longer K is walked in super-chunks.
 static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tokens, bool plain) {
     const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
     const int cols = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;  // wave columns over the tiles
@@ -245,12 +248,17 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
     }
     const size_t per_group = std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's activations
     const int wt = std::max(1, std::min({tokens <= 2 ? 2 : 8, cols, ctx->skinny_max_w}));
+    const long wgs = (cols + wt - 1) / wt;
+    // wave rows: dividing the chunks of K, within the wave and LDS limits; the fewest that make a workgroup of at least
+    // 4 waves, more only while the launch has fewer than skinny_fill waves per CU (measured: extra rows add LDS
+    // reductions and lose occupancy; fewer than 4 waves walk K in too many barrier-separated super-chunks)
+    const int nchunks = G / ng, wmax = std::min(ctx->skinny_max_w / wt, nchunks);
     int wk = 1;
-    for (int w = std::min(ctx->skinny_max_w / wt, G / ng); w >= 1; w--)
-        if ((G / ng) % w == 0 && (size_t)w * ng * per_group <= SKINNY_X_LDS) {
-            wk = w;
-            break;
-        }
+    for (int w = 1; w <= wmax; w++) {
+        if (nchunks % w || (size_t)w * ng * per_group > SKINNY_X_LDS) continue;
+        wk = w;
+        if (wt * w >= 4 && wgs * wt * w >= (long)ctx->skinny_fill * ctx->cus) break;
+    }
     return Partition{wt, wt * wk, 1, ng};
 }
 
