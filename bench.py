@@ -26,6 +26,7 @@ BF16_PEAK = 2500.0  # TFLOP/s dense, MI355X
 
 SET_27B = [(5120, 17408), (5120, 17408), (17408, 5120), (5120, 6144), (6144, 5120)]
 HEAD_27B = (5120, 248320)
+PREFILL_27B = [(5120, 17408), (17408, 5120), (5120, 6144)]
 
 
 def int4_bytes(k, n, m, zp=False):
@@ -239,6 +240,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
+    ap.add_argument("--prefill-run", action="store_true",
+                    help="the prefill profiling workload: 5 launches of each M=2048 prefill shape, no graph")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/*_traffic.json from the two --pmc runs' output directories")
     args = ap.parse_args()
@@ -261,6 +264,15 @@ def main():
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
         traffic_run(gemm, set_mats)
+        return
+    if args.prefill_run:
+        for i, (k, n) in enumerate(PREFILL_27B):
+            st = Step(gemm, 2048, k)
+            st.add(set_mats[[0, 2, 3][i]][0], Epi.Plain, int4_bytes(k, n, 2048), 2 * 2048 * k * n)
+            for _ in range(5):
+                st.run()
+        torch.cuda.synchronize()
+        print(json.dumps({"prefill_run": "done"}))
         return
     head = upload_copies(gemm, quant(200, "i4", *HEAD_27B), 1)[0]
 
@@ -301,7 +313,7 @@ def main():
         print(f"# M=5: {ms5:.4f} ms/step, {extra['m5_GBps']} GB/s", file=sys.stderr, flush=True)
     if "prefill" in only:
         pf = {}
-        for i, (k, n) in enumerate([(5120, 17408), (17408, 5120), (5120, 6144)]):
+        for i, (k, n) in enumerate(PREFILL_27B):
             mat = set_mats[[0, 2, 3][i]][0]
             st = Step(gemm, 2048, k)
             st.add(mat, Epi.Plain, int4_bytes(k, n, 2048), 2 * 2048 * k * n)
