@@ -7,6 +7,7 @@ The host repacker is compiled without floating-point contraction so that its ari
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -15,7 +16,11 @@ BUILD = os.path.join(HERE, "_build")
 ARCH = os.environ.get("QWENNY_ARCH", "gfx950")
 
 HOST_SRC = ["host.cpp"]
-HIP_SRC = ["kernels.hip", "api.hip"]
+HIP_SRC = ["api.hip"]
+# kernels.hip is compiled once per (storage format, epilogue) pair and once for the dispatcher, in parallel; the
+# formats are the F_* combinations that kernels.hip's launch() dispatches.
+KERNEL_FORMATS = {"i4": 0, "i4s32": 4, "zp": 2, "zps32": 6, "i8": 5, "i8perch": 13}
+KERNEL_EPIS = {"plain": 0, "silu": 1, "argmax": 2}
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -37,15 +42,26 @@ def build(verbose=False, out=LIB, defines=()):
     build_dir = BUILD if out == LIB else out + ".build"
     os.makedirs(build_dir, exist_ok=True)
     extra = [f"-D{d}" for d in defines]
-    objs = []
+    jobs = []
     for src in HOST_SRC:
         obj = os.path.join(build_dir, src + ".o")
-        _run([hipcc, *COMMON, "-ffp-contract=off", "-pthread", "-c", os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+        jobs.append((obj, [hipcc, *COMMON, "-ffp-contract=off", "-pthread", "-c", os.path.join(CSRC, src), "-o", obj]))
     for src in HIP_SRC:
         obj = os.path.join(build_dir, src + ".o")
-        _run([hipcc, *COMMON, *DEVICE, *extra, "-c", "-x", "hip", os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+        jobs.append((obj, [hipcc, *COMMON, *DEVICE, *extra, "-c", "-x", "hip", os.path.join(CSRC, src), "-o", obj]))
+    kern = os.path.join(CSRC, "kernels.hip")
+    parts = [("dispatch", ["-DQH_PART_DISPATCH"])]
+    parts += [(f"{f}_{e}", [f"-DQH_PART_F={fv}", f"-DQH_PART_EPI={ev}"])
+              for f, fv in KERNEL_FORMATS.items() for e, ev in KERNEL_EPIS.items()]
+    for name, defs in parts:
+        obj = os.path.join(build_dir, f"kernels_{name}.o")
+        jobs.append((obj, [hipcc, *COMMON, *DEVICE, *extra, *defs, "-c", "-x", "hip", kern, "-o", obj]))
+    # the largest objects first; workers: this machine's cores, at most 16
+    jobs.sort(key=lambda j: "plain" not in j[0] and "silu" not in j[0] and "argmax" not in j[0])
+    workers = max(1, min(16, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(_run, [cmd for _, cmd in jobs]))
+    objs = [obj for obj, _ in jobs]
     tmp = out + ".tmp"
     _run([hipcc, *DEVICE, "-shared", "-pthread", "-o", tmp, *objs])
     os.replace(tmp, out)

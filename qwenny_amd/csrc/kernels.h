@@ -61,7 +61,14 @@ constexpr size_t SKINNY_X_LDS = 64 * 1024;
 // Dynamic LDS of a skinny launch: the staged activations and the K reduction.
 size_t skinny_lds(const Launch& l);
 
-// The skinny kernel for m <= SKINNY_MAX_M, else the prefill kernel.
+enum { EPI_PLAIN = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
+
+// The kernels of one storage format F and epilogue EPI: the skinny kernel for m <= SKINNY_MAX_M, else the prefill
+// kernel.
+template <int F, int EPI>
+hipError_t launch_epi(const Launch& l);
+
+// launch_epi for l.fmt and l.epi.
 hipError_t launch(const Launch& l);
 
 }  // namespace qh

@@ -29,7 +29,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Kernel format F: bit flags of the storage (kernels.h F_*).
-enum { EPI_PLAIN = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
 
 __device__ __forceinline__ f32x4 mfma(u32x4 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
@@ -614,12 +613,6 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
 // ---------------------------------------------------------------------------------------------------------------
 // launchers
 
-size_t skinny_lds(const Launch& l) {
-    const int wk = l.waves / l.tile_waves;
-    const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
-    return x + (size_t)(wk - 1) * l.tile_waves * SKINNY_TILES * 4 * 64 * sizeof(float);
-}
-
 template <int F, int EPI, int NR, int NG>
 static hipError_t skinny_ng(const Launch& l) {
     const int tiles = l.rows / TILE;
@@ -680,10 +673,22 @@ static hipError_t prefill_epi(const Launch& l) {
     }
 }
 
+#if defined(QH_PART_F) && defined(QH_PART_EPI)
+// This object holds the kernels of one (format, epilogue) pair: the library compiles kernels.hip once per pair, in
+// parallel, plus once with QH_PART_DISPATCH for the dispatcher.
 template <int F, int EPI>
-static hipError_t launch_epi(const Launch& l) {
+hipError_t launch_epi(const Launch& l) {
     if (l.m <= SKINNY_MAX_M) return skinny_epi<F & ~F_PERCH, EPI>(l);
     return prefill_epi<F, EPI>(l);
+}
+template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(const Launch& l);
+#endif
+
+#ifdef QH_PART_DISPATCH
+size_t skinny_lds(const Launch& l) {
+    const int wk = l.waves / l.tile_waves;
+    const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
+    return x + (size_t)(wk - 1) * l.tile_waves * SKINNY_TILES * 4 * 64 * sizeof(float);
 }
 
 template <int F>
@@ -706,5 +711,6 @@ hipError_t launch(const Launch& l) {
         default: return hipErrorInvalidValue;
     }
 }
+#endif
 
 }  // namespace qh
