@@ -24,6 +24,10 @@ struct qh_ctx {
     int skinny_fill;        // skinny kernel, non-plain epilogues: waves per CU a launch aims for
     int skinny_tile_waves;  // skinny kernel, plain products: waves side by side over tiles (0: by token count)
     int pf_shape;           // prefill workgroup shape (0: by tail waste; QH_PF_SHAPE for tuning sweeps)
+    // prefill stream-K: partial tiles, then PF_SK_ITEMS_MAX item counters (zeroed here, left zero by every launch);
+    // QH_PF_SK=0 turns it off (tuning)
+    void* sk_scratch;
+    int stream_k;
 };
 
 static int env_int(const char* name, int dflt) {
@@ -66,16 +70,29 @@ extern "C" int qh_open(int device, qh_ctx** out) {
         (void)hipFree(scratch);
         return fail(QH_EHIP, "argmax scratch: clear failed");
     }
+    void* sk = nullptr;
+    const size_t sk_bytes = PF_SK_PART_BYTES + PF_SK_ITEMS_MAX * sizeof(unsigned);
+    if (hipMalloc(&sk, sk_bytes) != hipSuccess) {
+        (void)hipFree(scratch);
+        return fail(QH_ENOMEM, "prefill scratch of %zu bytes: allocation failed", sk_bytes);
+    }
+    if (hipMemset((uint8_t*)sk + PF_SK_PART_BYTES, 0, PF_SK_ITEMS_MAX * sizeof(unsigned)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(scratch);
+        (void)hipFree(sk);
+        return fail(QH_EHIP, "prefill scratch: clear failed");
+    }
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
                       std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
-                      std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0)))};
+                      std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, env_int("QH_PF_SK", 1) != 0};
     return QH_OK;
 }
 
 extern "C" void qh_close(qh_ctx* ctx) {
     if (!ctx) return;
     if (ctx->argmax_scratch) (void)hipFree(ctx->argmax_scratch);
+    if (ctx->sk_scratch) (void)hipFree(ctx->sk_scratch);
     delete ctx;
 }
 
@@ -315,6 +332,9 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     l.bf16_magic = 0x43004300u;
     l.cus = ctx->cus;
     l.pf_shape = ctx->pf_shape;
+    l.sk_part = (float*)ctx->sk_scratch;
+    l.sk_count = (unsigned*)((uint8_t*)ctx->sk_scratch + PF_SK_PART_BYTES);
+    l.stream_k = ctx->stream_k;
     l.nib_mask = 0x000F000Fu;
     if (m <= (size_t)SKINNY_MAX_M) {
         Partition p = skinny_partition(ctx, w, m, epi == QH_EPI_PLAIN && !whole);

@@ -38,6 +38,13 @@ struct Launch {
     int groups_per_wave;    // skinny kernel: 4, or 1 when the group count is not a multiple of 4
     int cus;                // compute units (the prefill shape choice)
     int pf_shape;           // prefill workgroup shape: 0 chosen by size, else forced (kernels.hip prefill_epi)
+    // prefill stream-K (kernels.hip prefill_kernel): scratch of partial tiles (PF_SK_PART_BYTES) and PF_SK_ITEMS_MAX
+    // item counters (zero between launches); stream_k = 0 turns it off. Set by the launcher: dp_items, sk_items,
+    // sk_wgs and the stream-K ranges (sk_q units per workgroup, one more for the first sk_r).
+    float* sk_part;
+    unsigned* sk_count;
+    int stream_k;
+    int dp_items, sk_items, sk_wgs, sk_q, sk_r;
     uint32_t bf16_magic;    // 0x43004300: the bf16 pair (128, 128) (see kernels.hip i4_biased)
     uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;
@@ -47,6 +54,12 @@ struct Launch {
 // it takes at most (the reference's MAX_OUT).
 constexpr int ARGMAX_SPREAD = 64;
 constexpr int ARGMAX_MAX_TOK = 64;
+
+// Prefill stream-K scratch: bytes of partial tiles (two slots per stream-K workgroup of a launch) and item counters.
+constexpr size_t PF_SK_PART_BYTES = (size_t)128 << 20;
+constexpr int PF_SK_ITEMS_MAX = 4096;
+// Cost of stream-K's partials in units of one group's compute (the launcher's choice between whole items and stream-K).
+constexpr int PF_SK_FIXUP = 12;
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
 constexpr int SKINNY_MAX_M = 16;

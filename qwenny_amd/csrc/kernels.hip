@@ -396,8 +396,18 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
 // A workgroup of WM x WN waves computes WM * BMB * 32 tokens x WN * TN * 32 outputs; wave (wm, wn) owns BMB token
 // blocks x TN output blocks (BMB * TN accumulators of 16 registers). Activations go through double-buffered,
 // XOR-swizzled LDS in stages of 64 columns; each wave dequantizes its outputs' weights straight from global memory into
-// bf16 registers ((q - z) s in f32, rounded once). Workgroups are ordered XCD-aware, token tiles fastest, so that
-// those sharing a weight tile share an XCD's L2.
+// bf16 registers ((q - z) s in f32, rounded once).
+//
+// Work distribution. A work item is one workgroup tile. Whole items go to the first dp_items workgroups, ordered
+// XCD-aware (token tiles fastest, so that workgroups sharing a weight tile share an XCD's L2). When whole items would
+// leave the last round of resident workgroups badly underfilled, the last sk_items items are instead spread evenly
+// over sk_wgs = P workgroups (one per resident slot) by groups of K ("stream-K"): of the U = sk_items * G
+// (item, group) units, range s takes a contiguous q = U / P of them, one more for the first r = U % P; ranges are
+// dealt to the workgroups XCD-aware too.
+// An item cut between workgroups is finished by the last of them to arrive: each writes its partial accumulators to
+// its own slot of a scratch buffer (device-coherent stores), then counts itself on the item's counter (a returning
+// device-scope atomic); the one that counts last adds the partials in segment order (so the sum does not depend on
+// who arrives last), runs the epilogue and clears the counter. No workgroup ever waits for another.
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -412,6 +422,13 @@ constexpr int PF_ROW = PF_BK * 2;  // LDS bytes per token row of a stage
 // 16 consecutive rows at one chunk hit all 64 banks once.
 __device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW + 16 * (kc ^ ((row >> 1) & 7)); }
 
+// Stream-K ranges: U units over P workgroups, q = U / P (at least 1) each and one more for the first r = U % P.
+// The first unit of workgroup s, and the workgroup whose range holds unit u:
+__device__ __forceinline__ int sk_begin(int s, int q, int r) { return s * q + min(s, r); }
+__device__ __forceinline__ int sk_owner(int u, int q, int r) {
+    return u < r * (q + 1) ? u / (q + 1) : r + (u - r * (q + 1)) / q;
+}
+
 template <int F, int EPI, int BMB, int TN, int WM, int WN>
 __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
     constexpr int NTHR = WM * WN * 64;
@@ -421,21 +438,19 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
     static_assert(CPT >= 1 && CPT * NTHR == BM * (PF_ROW / 16), "stage pieces must divide over the threads");
     constexpr int CW = CodeWords<F>::N;
     constexpr int STAGE = BM * PF_ROW;               // LDS bytes of one stage
+    constexpr int NW = WM * WN;                      // waves
+    constexpr int NACC = BMB * TN * 16;              // accumulator registers per lane
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+    __shared__ int sk_last;
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), tid = threadIdx.x;
     const int wm = wave % WM, wn = wave / WM;
     const int l32 = lane & 31, lh = lane >> 5, l16 = lane & 15;
     const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
 
-    // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous run of work items, token tiles
-    // fastest, so the workgroups sharing a weight tile share that XCD's L2.
-    const int nb = gridDim.x, b = blockIdx.x, xcd = b & 7, q8 = nb >> 3, r8 = nb & 7;
-    const int item = xcd * q8 + min(xcd, r8) + (b >> 3);
     const int ntok = (M + BM - 1) / BM;
-    const int tok0 = (item % ntok) * BM;
-    const int tile0 = (item / ntok) * WTILES + wn * TN * 2;  // the wave's first tile
-    const int wtok0 = wm * BMB * 32;                         // the wave's first token row in the stage
+    const int wtok0 = wm * BMB * 32;  // the wave's first token row in the stage
+    int tok0 = 0, tile0 = 0;          // the current item's first token and the wave's first tile
 
     // Global loads take a wave-uniform base plus a 32-bit per-lane byte offset fixed for the whole kernel (no 64-bit
     // address arithmetic per load). Activations: piece c = tid + NTHR i -> row c / 8, column chunk c % 8.
@@ -444,10 +459,8 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
     int xs[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
-        const int c = tid + NTHR * i, row = c >> 3, kc = c & 7;
-        const int tok = min(tok0 + row, M - 1);
-        xg[i] = (uint32_t)(((size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc) * 2);
-        xs[i] = pf_lds_off(row, kc);
+        const int c = tid + NTHR * i;
+        xs[i] = pf_lds_off(c >> 3, c & 7);
     }
     auto stage_load = [&](int s, u32x4 (&v)[CPT]) {
         const uint8_t* p = xbase + (size_t)s * PF_ROW;
@@ -467,13 +480,24 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
     // this lane's output row: tile tt[t] (of output block t), row l16; its code pieces and scales as offsets
     int tt[TN];
     uint32_t cg[TN], sg[TN], zg[TN];
+    // the per-lane offsets of an item
+    auto set_item = [&](int item) {
+        tok0 = (item % ntok) * BM;
+        tile0 = (item / ntok) * WTILES + wn * TN * 2;
 #pragma unroll
-    for (int t = 0; t < TN; t++) {
-        tt[t] = min(tile0 + 2 * t + (l32 >> 4), tiles - 1);
-        cg[t] = (uint32_t)(((size_t)tt[t] * G * 64 * CW + 16 * lh + l16) * 16);
-        sg[t] = (uint32_t)(scale_idx(tt[t], G, 0, l16) * ((F & F_S32) ? 4 : 2));
-        zg[t] = (uint32_t)(zero_idx(tt[t], G, 0, l16) * 2);
-    }
+        for (int i = 0; i < CPT; i++) {
+            const int c = tid + NTHR * i, row = c >> 3, kc = c & 7;
+            const int tok = min(tok0 + row, M - 1);
+            xg[i] = (uint32_t)(((size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc) * 2);
+        }
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            tt[t] = min(tile0 + 2 * t + (l32 >> 4), tiles - 1);
+            cg[t] = (uint32_t)(((size_t)tt[t] * G * 64 * CW + 16 * lh + l16) * 16);
+            sg[t] = (uint32_t)(scale_idx(tt[t], G, 0, l16) * ((F & F_S32) ? 4 : 2));
+            zg[t] = (uint32_t)(zero_idx(tt[t], G, 0, l16) * 2);
+        }
+    };
     struct WFrag {
         u32x4 c[TN][2][CW];  // per output block: the two pieces (x CW words for int8)
         float s[TN], off[TN];
@@ -510,12 +534,14 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
     };
 
     f32x16 acc[BMB][TN];
+    auto clear = [&]() {
 #pragma unroll
-    for (int bb = 0; bb < BMB; bb++)
+        for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
-        for (int t = 0; t < TN; t++)
+            for (int t = 0; t < TN; t++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) acc[bb][t][e] = 0.0f;
+                for (int e = 0; e < 16; e++) acc[bb][t][e] = 0.0f;
+    };
 
     // one stage (64 columns, half hh of the group) from LDS buffer `buf`: the A fragments of k16 step s16 + 1 are read
     // while step s16's MFMAs run
@@ -541,73 +567,146 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
         }
     };
 
-    // group g: stage 2g from buffer 0 while stage 2g + 1 is loaded, then stage 2g + 1 from buffer 1 while stage
-    // 2g + 2 is loaded; the next group's weights are loaded one group ahead
-    u32x4 xv[CPT];
-    WFrag wcur, wnxt;
-    stage_load(0, xv);
-    wload(0, wcur);
-    stage_store(0, xv);
-    __syncthreads();
-    for (int g = 0; g < G; g++) {
-        const bool more = g + 1 < G;
-        stage_load(2 * g + 1, xv);
-        wload(more ? g + 1 : g, wnxt);
-        compute(0, 0, wcur);
-        stage_store(1, xv);
+    // acc = the current item's product over groups [g0, g1). Group g: stage 2g from buffer 0 while stage 2g + 1 is
+    // loaded, then stage 2g + 1 from buffer 1 while stage 2g + 2 is loaded; the next group's weights are loaded one
+    // group ahead.
+    auto run = [&](int g0, int g1) {
+        clear();
+        u32x4 xv[CPT];
+        WFrag wcur, wnxt;
+        stage_load(2 * g0, xv);
+        wload(g0, wcur);
+        stage_store(0, xv);
         __syncthreads();
-        if (more) stage_load(2 * g + 2, xv);
-        compute(1, 1, wcur);
-        if (more) stage_store(0, xv);
-        __syncthreads();
-        wcur = wnxt;
-    }
+        for (int g = g0; g < g1; g++) {
+            const bool more = g + 1 < g1;
+            stage_load(2 * g + 1, xv);
+            wload(more ? g + 1 : g, wnxt);
+            compute(0, 0, wcur);
+            stage_store(1, xv);
+            __syncthreads();
+            if (more) stage_load(2 * g + 2, xv);
+            compute(1, 1, wcur);
+            if (more) stage_store(0, xv);
+            __syncthreads();
+            wcur = wnxt;
+        }
+    };
 
-    // epilogue: acc[bb][t][v] = D[token tok0 + wtok0 + 32 bb + 8 (v / 4) + 4 lh + v % 4][output 32-block t, l32]
-    float rs[TN];
+    // epilogue of the current item: acc[bb][t][v] = D[token tok0 + wtok0 + 32 bb + 8 (v / 4) + 4 lh + v % 4]
+    // [output 32-block t, l32]
+    auto epilogue = [&]() {
+        float rs[TN];
 #pragma unroll
-    for (int t = 0; t < TN; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tt[t], G, 0, l16) : 1.0f;
-    unsigned long long key[BMB][16];
-#pragma unroll
-    for (int bb = 0; bb < BMB; bb++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) key[bb][v] = 0;
-#pragma unroll
-    for (int t = 0; t < TN; t++) {
-        const int tile = tile0 + 2 * t + (l32 >> 4);
-        const bool tile_ok = tile < tiles;
-        const int out = tile * TILE + l16;
+        for (int t = 0; t < TN; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tt[t], G, 0, l16) : 1.0f;
+        unsigned long long key[BMB][16];
 #pragma unroll
         for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
-                const float val = (F & F_PERCH) ? acc[bb][t][v] * rs[t] : acc[bb][t][v];
-                if (EPI == EPI_SILU) {
-                    const float up = __shfl_xor(val, 8);
-                    if (tile_ok && l16 < 8 && tok < M)
-                        ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(val) * up);
-                } else {
-                    if (tile_ok && tok < M) ((float*)a.y)[(size_t)tok * a.ldy + out] = val;
-                    if (EPI == EPI_ARGMAX && tile_ok && tok < M && out < a.valid)
-                        key[bb][v] = max_u64(key[bb][v], argmax_key(val, out));
+            for (int v = 0; v < 16; v++) key[bb][v] = 0;
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            const int tile = tile0 + 2 * t + (l32 >> 4);
+            const bool tile_ok = tile < tiles;
+            const int out = tile * TILE + l16;
+#pragma unroll
+            for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
+                    const float val = (F & F_PERCH) ? acc[bb][t][v] * rs[t] : acc[bb][t][v];
+                    if (EPI == EPI_SILU) {
+                        const float up = __shfl_xor(val, 8);
+                        if (tile_ok && l16 < 8 && tok < M)
+                            ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(val) * up);
+                    } else {
+                        if (tile_ok && tok < M) ((float*)a.y)[(size_t)tok * a.ldy + out] = val;
+                        if (EPI == EPI_ARGMAX && tile_ok && tok < M && out < a.valid)
+                            key[bb][v] = max_u64(key[bb][v], argmax_key(val, out));
+                    }
                 }
-            }
+        }
+        if (EPI == EPI_ARGMAX) {
+            // the max over the 32 lanes that share a token (one lane half)
+#pragma unroll
+            for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    unsigned long long k = key[bb][v];
+#pragma unroll
+                    for (int o = 1; o < 32; o <<= 1) k = max_u64(k, __shfl_xor(k, o));
+                    const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
+                    if (l32 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
+                }
+        }
+    };
+
+    // This workgroup's units (item * G + group): one whole item for the first dp_items workgroups, XCD-aware
+    // (workgroup b runs on XCD b % 8; each XCD gets a contiguous run of items), else its stream-K range.
+    const int b = blockIdx.x, dp = a.dp_items;
+    int u, u1, s = -1;
+    if (b < dp) {
+        const int xcd = b & 7, q8 = dp >> 3, r8 = dp & 7;
+        u = (xcd * q8 + min(xcd, r8) + (b >> 3)) * G;
+        u1 = u + G;
+    } else {
+        // stream-K range s, XCD-aware like whole items: workgroups b and b + 8 run on one XCD, and each XCD takes a
+        // contiguous run of ranges (so the items they cut share its L2)
+        const int c = b - dp, xcd = c & 7, q8 = a.sk_wgs >> 3, r8 = a.sk_wgs & 7;
+        s = xcd * q8 + min(xcd, r8) + (c >> 3);
+        u = dp * G + sk_begin(s, a.sk_q, a.sk_r);
+        u1 = dp * G + sk_begin(s + 1, a.sk_q, a.sk_r);
     }
-    if (EPI == EPI_ARGMAX) {
-        // the max over the 32 lanes that share a token (one lane half)
+    const int first_item = u / G;
+    while (u < u1) {
+        const int it = u / G, g0 = u - it * G, g1 = min(G, g0 + (u1 - u));
+        set_item(it);
+        run(g0, g1);
+        u += g1 - g0;
+        if (g0 != 0 || g1 != G) {
+            // a cut item (stream-K): write this segment's partial to slot 2 s (+1 unless it is this workgroup's
+            // first item), as [wave][register][lane] f32, with device-coherent stores
+            float* part = a.sk_part + ((size_t)(2 * s + (it != first_item)) * NW + wave) * NACC * 64 + lane;
 #pragma unroll
-        for (int bb = 0; bb < BMB; bb++)
+            for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                unsigned long long k = key[bb][v];
+                for (int t = 0; t < TN; t++)
 #pragma unroll
-                for (int o = 1; o < 32; o <<= 1) k = max_u64(k, __shfl_xor(k, o));
-                const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (l32 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
+                    for (int e = 0; e < 16; e++)
+                        __hip_atomic_store(part + ((bb * TN + t) * 16 + e) * 64, acc[bb][t][e], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's partial has been performed
+            __syncthreads();
+            const int sit = it - dp, su = sit * G;  // the item among the stream-K ones, its first unit
+            const int sa = sk_owner(su, a.sk_q, a.sk_r), sb = sk_owner(su + G - 1, a.sk_q, a.sk_r);
+            if (threadIdx.x == 0)
+                sk_last = __hip_atomic_fetch_add(a.sk_count + sit, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(sb - sa);
+            __syncthreads();
+            if (!sk_last) continue;  // uniform over the workgroup
+            // the last segment to arrive: sum the partials in segment order (its own read back like the others, so
+            // that the sum does not depend on the order of arrival), 16 registers at a time
+            clear();
+            for (int o = sa; o <= sb; o++) {
+                const int slot = 2 * o + (sk_begin(o, a.sk_q, a.sk_r) < su);
+                const float* src = a.sk_part + ((size_t)slot * NW + wave) * NACC * 64 + lane;
+#pragma unroll
+                for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+                    for (int t = 0; t < TN; t++) {
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            acc[bb][t][e] += __hip_atomic_load(src + ((bb * TN + t) * 16 + e) * 64,
+                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
             }
-        argmax_finish(a);
+            if (threadIdx.x == 0)
+                (void)__hip_atomic_exchange(a.sk_count + sit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        epilogue();
     }
+    if (EPI == EPI_ARGMAX) argmax_finish(a);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -639,11 +738,44 @@ static hipError_t skinny_epi(const Launch& l) {
 }
 
 template <int F, int EPI, int BMB, int TN, int WM, int WN>
-static hipError_t prefill_cfg(const Launch& l) {
-    const int tiles = l.rows / TILE;
-    const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32;
-    const int items = ((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
-    hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN>), dim3(items), dim3(WM * WN * 64), 0, l.stream, l);
+static hipError_t prefill_cfg(const Launch& l0) {
+    Launch l = l0;
+    const int tiles = l.rows / TILE, G = l.cols / QG;
+    const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32, threads = WM * WN * 64;
+    const long items = (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
+    auto kern = prefill_kernel<F, EPI, BMB, TN, WM, WN>;
+    // Stream-K: the last P < sk_items <= 2 P items (all of them when there are at most 2 P) are spread over P = the
+    // resident workgroups, when that is estimated faster in units of one group's compute: whole items take rounds * G;
+    // stream-K takes (rounds - 2) * G for the whole rounds, ceil(U / P) for the spread units and PF_SK_FIXUP for
+    // writing and summing the partials of cut items (measured on MI355X: a 256 x 256 partial costs about as much as
+    // 12 groups of K, so a 75%-full single round of K = 5120 stays whole).
+    static int per_cu = -1;  // resident workgroups per CU (per instantiation; the same on every MI355X)
+    if (per_cu < 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess) n = 0;
+        per_cu = n;
+    }
+    const long P = (long)per_cu * l.cus;
+    l.dp_items = (int)items;
+    l.sk_items = 0;
+    l.sk_wgs = 0;
+    if (l.stream_k && P > 0) {
+        const long rounds = (items + P - 1) / P;
+        const size_t slot = (size_t)bm * wg_tiles * TILE * 4;
+        const long sk = rounds >= 2 ? items - (rounds - 2) * P : items;
+        const long U = sk * G;
+        const long t_dp = rounds * G, t_sk = (rounds >= 2 ? (rounds - 2) * G : 0) + (U + P - 1) / P + PF_SK_FIXUP;
+        if (t_sk * 20 < t_dp * 19 && 2 * P * slot <= PF_SK_PART_BYTES) {
+            if (sk <= PF_SK_ITEMS_MAX && U >= P && items * G < (1l << 31)) {
+                l.dp_items = (int)(items - sk);
+                l.sk_items = (int)sk;
+                l.sk_wgs = (int)P;
+                l.sk_q = (int)(U / P);
+                l.sk_r = (int)(U % P);
+            }
+        }
+    }
+    hipLaunchKernelGGL(kern, dim3(l.dp_items + l.sk_wgs), dim3(threads), 0, l.stream, l);
     return hipGetLastError();
 }
 
