@@ -231,6 +231,36 @@ def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
     print(json.dumps(res))
 
 
+def summarize_clock(pmc_dir, min_ns=50000):
+    """Per kernel (name, grid) of a rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: mean duration, the
+    clock it ran at (GRBM_GUI_ACTIVE sums the 8 XCDs' cycles) and the fraction of cycles each SIMD's MFMA unit was busy
+    (the counter sums the 1024 SIMDs). Dispatches shorter than min_ns are left out."""
+    import collections
+    import glob
+    import sqlite3
+
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    meta = {}
+    for db in glob.glob(os.path.join(pmc_dir, "**", "*_results.db"), recursive=True):
+        c = sqlite3.connect(db)
+        for disp, name, cn, v, du, grid in c.execute(
+                "select dispatch_id, kernel_name, counter_name, value, duration, grid_size from counters_collection"):
+            per[(db, disp)][cn] += v
+            meta[(db, disp)] = (name, grid, du)
+    rows = collections.defaultdict(list)
+    for key, cnt in per.items():
+        name, grid, du = meta[key]
+        if du >= min_ns and cnt.get("GRBM_GUI_ACTIVE"):
+            cyc = cnt["GRBM_GUI_ACTIVE"] / 8
+            rows[(name.split("(")[0][:70], grid)].append((du, cyc / du, cnt.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / 1024 / cyc))
+    print("| Kernel | Grid (threads) | Dispatches | Mean duration (us) | Clock (GHz) | MFMA busy per SIMD |")
+    print("|---|---|---|---|---|---|")
+    for (name, grid), v in sorted(rows.items()):
+        n = len(v)
+        print(f"| `{name}` | {grid} | {n} | {sum(x[0] for x in v) / n / 1e3:.1f} | {sum(x[1] for x in v) / n:.2f} | "
+              f"{sum(x[2] for x in v) / n:.3f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,11 +270,19 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
+    ap.add_argument("--with-torch", action="store_true",
+                    help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
     ap.add_argument("--prefill-run", action="store_true",
                     help="the prefill profiling workload: 5 launches of each M=2048 prefill shape, no graph")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/*_traffic.json from the two --pmc runs' output directories")
+    ap.add_argument("--summarize-clock", metavar="PMC_DIR",
+                    help="print per-kernel clock and MFMA busy from a --kernel-trace --pmc GRBM_GUI_ACTIVE "
+                         "SQ_VALU_MFMA_BUSY_CYCLES run's output directory (markdown)")
     args = ap.parse_args()
+    if args.summarize_clock:
+        summarize_clock(args.summarize_clock)
+        return
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic)
         return
@@ -271,6 +309,11 @@ def main():
             st.add(set_mats[[0, 2, 3][i]][0], Epi.Plain, int4_bytes(k, n, 2048), 2 * 2048 * k * n)
             for _ in range(5):
                 st.run()
+            if args.with_torch:  # the same shape as a dense bf16 product through torch (hipBLASLt), for comparison
+                a = torch.randn(2048, k, device="cuda").to(torch.bfloat16)
+                b = torch.randn(n, k, device="cuda").to(torch.bfloat16)
+                for _ in range(5):
+                    a @ b.t()
         torch.cuda.synchronize()
         print(json.dumps({"prefill_run": "done"}))
         return

@@ -5,7 +5,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.environ.get("QWENNY_HIP_LIB") or os.path.join(HERE, "libqwenny_hip.so")
+LIB_PATH = os.environ.get("QWENNY_HIP_LIB") or os.path.join(HERE, "libqwenny_hip.so")  # QWENNY_HIP_LIB: another build (tuning)
 
 P, S, I, U64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64
 

@@ -191,10 +191,11 @@ class Mat:
     def __init__(self, gemm, handle):
         self._gemm = gemm
         self._m = handle
+        self._free = lib().qh_mat_free  # bound now: at interpreter exit the module globals may already be gone
 
     def __del__(self):
         if getattr(self, "_m", None):
-            lib().qh_mat_free(self._m)
+            self._free(self._m)
             self._m = None
 
     def desc(self):

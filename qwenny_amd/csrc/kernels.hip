@@ -263,7 +263,6 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
             }
         // 3. stage the activations
         if (c > c0) __syncthreads();  // the previous super-chunk's readers are done
-#ifndef QH_EXP_NOX
 #pragma unroll
         for (int i = 0; i < XPT; i++)
             if (xo[i] >= 0) *(u32x4*)(xs_lds + xo[i]) = xv[i];
@@ -273,17 +272,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
                 (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
             *(u32x4*)(xs_lds + (size_t)tok * xpitch + 8 * pc) = *(const u32x4*)src;
         }
-#endif
         __syncthreads();
-#ifdef QH_EXP_NOCOMP
-        {
-            uint32_t h = 0;
-            for (int gi = 0; gi < NG; gi++)
-                for (int t = 0; t < T; t++) h ^= code[gi][t][0].x ^ code[gi][t][0].y ^ code[gi][t][0].z ^ code[gi][t][0].w ^ sraw[t][0];
-            acc[0][0] += __uint_as_float(h & 0x3fffffffu);
-            continue;
-        }
-#endif
         // 3. compute the wave's groups
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
@@ -415,12 +404,22 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
 }
 
-constexpr int PF_BK = 64;          // columns per LDS stage (half a group)
-constexpr int PF_ROW = PF_BK * 2;  // LDS bytes per token row of a stage
+#ifndef QH_PF_BK
+#define QH_PF_BK 64
+#endif
 
-// LDS byte offset of 16-byte chunk kc (0..7) of token row `row` in a stage: XOR-swizzled so that 16 lanes reading
-// 16 consecutive rows at one chunk hit all 64 banks once.
-__device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW + 16 * (kc ^ ((row >> 1) & 7)); }
+constexpr int PF_BK = QH_PF_BK;      // columns per LDS stage (64: half a group, or 128)
+constexpr int PF_ROW = PF_BK * 2;    // LDS bytes per token row of a stage
+constexpr int PF_KC = PF_BK / 8;     // 16-byte chunks per row of a stage
+constexpr int PF_SPG = QG / PF_BK;   // stages per group
+constexpr int PF_K16 = PF_BK / 16;   // k16 steps per stage
+static_assert(PF_SPG * PF_BK == QG && (PF_KC == 8 || PF_KC == 16), "a stage is half a group or one group");
+
+// LDS byte offset of 16-byte chunk kc of token row `row` in a stage: XOR-swizzled so that 16 lanes reading 16
+// consecutive rows at one chunk hit all 64 banks once (rows of 128 bytes pair up in one 256-byte bank line).
+__device__ __forceinline__ int pf_lds_off(int row, int kc) {
+    return row * PF_ROW + 16 * (PF_KC == 8 ? kc ^ ((row >> 1) & 7) : kc ^ (row & 15));
+}
 
 // Stream-K ranges: U units over P workgroups, q = U / P (at least 1) each and one more for the first r = U % P.
 // The first unit of workgroup s, and the workgroup whose range holds unit u:
@@ -429,8 +428,8 @@ __device__ __forceinline__ int sk_owner(int u, int q, int r) {
     return u < r * (q + 1) ? u / (q + 1) : r + (u - r * (q + 1)) / q;
 }
 
-template <int F, int EPI, int BMB, int TN, int WM, int WN>
-__global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
+template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB>
+__global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     constexpr int NTHR = WM * WN * 64;
     constexpr int BM = WM * BMB * 32;                // tokens per workgroup
     constexpr int WTILES = WN * TN * 2;              // 16-row tiles per workgroup
@@ -460,7 +459,7 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
         const int c = tid + NTHR * i;
-        xs[i] = pf_lds_off(c >> 3, c & 7);
+        xs[i] = pf_lds_off(c / PF_KC, c % PF_KC);
     }
     auto stage_load = [&](int s, u32x4 (&v)[CPT]) {
         const uint8_t* p = xbase + (size_t)s * PF_ROW;
@@ -473,9 +472,9 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
     };
     // LDS reads of A fragments: row wtok0 + 32 bb + l32, chunk 2 s16 + lh; the swizzle of rows 32 bb + l32 depends on
     // l32 only, so the per-lane part is 4 offsets and the token block is an immediate
-    int xr[4];
+    int xr[PF_K16];
 #pragma unroll
-    for (int s16 = 0; s16 < 4; s16++) xr[s16] = pf_lds_off(wtok0 + l32, 2 * s16 + lh);
+    for (int s16 = 0; s16 < PF_K16; s16++) xr[s16] = pf_lds_off(wtok0 + l32, 2 * s16 + lh);
 
     // this lane's output row: tile tt[t] (of output block t), row l16; its code pieces and scales as offsets
     int tt[TN];
@@ -486,7 +485,7 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
         tile0 = (item / ntok) * WTILES + wn * TN * 2;
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
-            const int c = tid + NTHR * i, row = c >> 3, kc = c & 7;
+            const int c = tid + NTHR * i, row = c / PF_KC, kc = c % PF_KC;
             const int tok = min(tok0 + row, M - 1);
             xg[i] = (uint32_t)(((size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc) * 2);
         }
@@ -551,15 +550,15 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
 #pragma unroll
         for (int bb = 0; bb < BMB; bb++) xa[0][bb] = *(const u32x4*)(lb + xr[0] + bb * 32 * PF_ROW);
 #pragma unroll
-        for (int s16 = 0; s16 < 4; s16++) {
-            if (s16 < 3) {
+        for (int s16 = 0; s16 < PF_K16; s16++) {
+            if (s16 < PF_K16 - 1) {
 #pragma unroll
                 for (int bb = 0; bb < BMB; bb++)
                     xa[(s16 + 1) & 1][bb] = *(const u32x4*)(lb + xr[s16 + 1] + bb * 32 * PF_ROW);
             }
             bf16x8 bw[TN];
 #pragma unroll
-            for (int t = 0; t < TN; t++) bw[t] = dequant(w, t, 4 * hh + s16);
+            for (int t = 0; t < TN; t++) bw[t] = dequant(w, t, PF_K16 * hh + s16);
 #pragma unroll
             for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
@@ -567,28 +566,31 @@ __global__ __launch_bounds__(WM * WN * 64) void prefill_kernel(Launch a) {
         }
     };
 
-    // acc = the current item's product over groups [g0, g1). Group g: stage 2g from buffer 0 while stage 2g + 1 is
-    // loaded, then stage 2g + 1 from buffer 1 while stage 2g + 2 is loaded; the next group's weights are loaded one
+    // acc = the current item's product over groups [g0, g1): stage s is computed from one LDS buffer while stage
+    // s + 1 is loaded into registers and then stored to the other buffer; the next group's weights are loaded one
     // group ahead.
     auto run = [&](int g0, int g1) {
         clear();
         u32x4 xv[CPT];
         WFrag wcur, wnxt;
-        stage_load(2 * g0, xv);
+        const int s1 = g1 * PF_SPG;  // stages of [g0, g1): stage s holds columns s * PF_BK ..
+        int buf = 0;
+        stage_load(g0 * PF_SPG, xv);
         wload(g0, wcur);
         stage_store(0, xv);
         __syncthreads();
         for (int g = g0; g < g1; g++) {
-            const bool more = g + 1 < g1;
-            stage_load(2 * g + 1, xv);
-            wload(more ? g + 1 : g, wnxt);
-            compute(0, 0, wcur);
-            stage_store(1, xv);
-            __syncthreads();
-            if (more) stage_load(2 * g + 2, xv);
-            compute(1, 1, wcur);
-            if (more) stage_store(0, xv);
-            __syncthreads();
+#pragma unroll
+            for (int hh = 0; hh < PF_SPG; hh++) {
+                const int s = g * PF_SPG + hh;
+                const bool more = s + 1 < s1;
+                if (more) stage_load(s + 1, xv);
+                if (hh == 0) wload(g + 1 < g1 ? g + 1 : g, wnxt);
+                compute(buf, hh, wcur);
+                if (more) stage_store(buf ^ 1, xv);
+                __syncthreads();
+                buf ^= 1;
+            }
             wcur = wnxt;
         }
     };
@@ -737,13 +739,13 @@ static hipError_t skinny_epi(const Launch& l) {
     }
 }
 
-template <int F, int EPI, int BMB, int TN, int WM, int WN>
+template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB = 1>
 static hipError_t prefill_cfg(const Launch& l0) {
     Launch l = l0;
     const int tiles = l.rows / TILE, G = l.cols / QG;
     const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32, threads = WM * WN * 64;
     const long items = (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
-    auto kern = prefill_kernel<F, EPI, BMB, TN, WM, WN>;
+    auto kern = prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>;
     // Stream-K: the last P < sk_items <= 2 P items (all of them when there are at most 2 P) are spread over P = the
     // resident workgroups, when that is estimated faster in units of one group's compute: whole items take rounds * G;
     // stream-K takes (rounds - 2) * G for the whole rounds, ceil(U / P) for the spread units and PF_SK_FIXUP for
