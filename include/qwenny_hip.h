@@ -37,7 +37,8 @@ enum qh_wt {
     QH_WT_I4 = 2,  /* symmetric int4 (zero point 8), bf16 scale per row and 128 columns (core.rs Wt::Marlin) */
     QH_WT_I4Z = 3, /* int4 with a 4-bit zero point per row and 128 columns (core.rs Wt::MarlinZ) */
     QH_WT_I4_S32 = 4, /* QH_WT_I4 with f32 scales: scales that bf16 does not hold exactly (f16 / f32 checkpoints) */
-    QH_WT_I4Z_S32 = 5 /* QH_WT_I4Z with f32 scales */
+    QH_WT_I4Z_S32 = 5, /* QH_WT_I4Z with f32 scales */
+    QH_WT_BF16 = 6     /* dense 16-bit weights kept bf16, no scales (core.rs Wt::F16, which rounds them to f16) */
 };
 
 /* Epilogue of a product (core.rs:52-58 `Epi`). */
@@ -121,6 +122,13 @@ int qh_unpack_row(int wt, size_t rows, size_t cols, const void* codes, const voi
 int qh_pack_dense_int8(const uint16_t* bf16, size_t rows, size_t cols, const size_t* order, size_t n, void* codes,
                        void* scales);
 
+/* Mat::new / pack 16-bit branch (core.rs:127-135, :370-381): dense bf16 [rows][cols] rows `order` into the
+ * QH_WT_BF16 layout, bit for bit (the reference rounds them to f16). codes: qh_packed_sizes bytes. */
+int qh_pack_dense_bf16(const uint16_t* bf16, size_t rows, size_t cols, const size_t* order, size_t n, void* codes);
+
+/* The inverse for one packed row p of a QH_WT_BF16 matrix: its bf16 values into out[cols]. */
+int qh_unpack_row_bf16(size_t rows, size_t cols, const void* codes, size_t p, uint16_t* out);
+
 /* ---- device: context, matrices, products ---------------------------------------------------------------------- */
 
 /* Gemm::load (core.rs:436-481): a context on `device` (makes it current on this thread). */
@@ -143,6 +151,10 @@ int qh_mat_quant_rows(qh_ctx* ctx, const qh_quant* q, const uint8_t* zeros, cons
 
 /* Mat::new int8 (core.rs:127-135): dense bf16 [rows][cols] requantized to int8 (qh_pack_dense_int8), uploaded. */
 int qh_mat_dense_int8(qh_ctx* ctx, const uint16_t* bf16, size_t rows, size_t cols, int silu, qh_mat** out);
+
+/* Mat::new with int8 false (core.rs:127-135, Wt::F16): dense bf16 [rows][cols] packed in row_order(silu) as
+ * QH_WT_BF16 (qh_pack_dense_bf16) and uploaded; the 16-bit matrices of a pre-quantized checkpoint (in_ba). */
+int qh_mat_dense(qh_ctx* ctx, const uint16_t* bf16, size_t rows, size_t cols, int silu, qh_mat** out);
 
 void qh_mat_free(qh_mat* m);
 int qh_mat_describe(const qh_mat* m, qh_mat_desc* out);

@@ -126,6 +126,19 @@ def gemm_f32(bits, group, q, scales, offsets, x_bf16, threads=1):
     return y
 
 
+def dense_f64(w_bf16, x_bf16, f16_weights=False):
+    """The dense 16-bit product y[t][r] = sum_c x[t][c] w[r][c] in f64 (src/cuda/core.rs:370-381 packs the weights,
+    kernels/gemm.cuh:120-212 multiplies them); w, x bf16 bits. `f16_weights`: the reference's storage, which rounds
+    each weight to f16 (half::f16::from_f32, nearest even) before the product."""
+    w = np.asarray(w_bf16, np.uint16).astype(np.uint32) << 16
+    w = w.view(np.float32)
+    if f16_weights:
+        with np.errstate(over="ignore"):  # beyond 65504: infinity, as the reference's f16 storage
+            w = w.astype(np.float16).astype(np.float32)
+    x = (np.asarray(x_bf16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return x.astype(np.float64) @ w.astype(np.float64).T
+
+
 # ---- epilogues (numpy restatements) ---------------------------------------------------------------------------
 
 

@@ -1,11 +1,12 @@
 """qwenny_amd: MI355X (gfx950) quantized-weight matrix products for qwenny's Qwen3.5 stack.
 
 W4A16 (group-128 int4, compressed-tensors pack-quantized, symmetric or with packed int4 zero points) and W8A16 (int8)
-products in hand-written HIP behind a C ABI (include/qwenny_hip.h, libqwenny_hip.so); this package is the host-side
+products, and the dense 16-bit products of the same call sites, in hand-written HIP behind a C ABI (include/qwenny_hip.h, libqwenny_hip.so); this package is the host-side
 mirror of the reference's `Mat` / `Gemm` runtime and checkpoint formats.
 """
 
-from .core import Epi, Gemm, Mat, Quant, Wt, pack_dense_int8, pack_quant, packed_sizes, row_order, unpack_rows
+from .core import (Epi, Gemm, Mat, Quant, Wt, pack_dense_bf16, pack_dense_int8, pack_quant, packed_sizes, row_order,
+                   unpack_rows, unpack_rows_bf16)
 
-__all__ = ["Epi", "Gemm", "Mat", "Quant", "Wt", "pack_dense_int8", "pack_quant", "packed_sizes", "row_order",
-           "unpack_rows"]
+__all__ = ["Epi", "Gemm", "Mat", "Quant", "Wt", "pack_dense_bf16", "pack_dense_int8", "pack_quant", "packed_sizes",
+           "row_order", "unpack_rows", "unpack_rows_bf16"]

@@ -19,7 +19,7 @@ HOST_SRC = ["host.cpp"]
 HIP_SRC = ["api.hip"]
 # kernels.hip is compiled once per (storage format, epilogue) pair and once for the dispatcher, in parallel; the
 # formats are the F_* combinations that kernels.hip's launch() dispatches.
-KERNEL_FORMATS = {"i4": 0, "i4s32": 4, "zp": 2, "zps32": 6, "i8": 5, "i8perch": 13}
+KERNEL_FORMATS = {"i4": 0, "i4s32": 4, "zp": 2, "zps32": 6, "i8": 5, "i8perch": 13, "bf16": 16}
 KERNEL_EPIS = {"plain": 0, "silu": 1, "argmax": 2}
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]

@@ -13,7 +13,7 @@ import numpy as np
 
 from ._lib import QuantC, check, lib
 from .core import Quant
-from .synth import bf16_to_f32
+from .synth import bf16_to_f32, f32_to_bf16
 
 
 def packed_scheme(qc):
@@ -165,6 +165,16 @@ class Checkpoint:
 
     def prequantized(self):
         return self.scheme is not None
+
+    def bf16(self, name):
+        """A 16-bit or f32 tensor as bf16 bits and its shape (src/checkpoint.rs Checkpoint::bf16): bf16 as stored,
+        f16 and f32 rounded to nearest even."""
+        raw = self._raw(name)
+        if raw is None:
+            raise KeyError(name)
+        dt, arr = raw
+        bits = arr.view(np.uint16) if dt == "BF16" else f32_to_bf16(_floats(arr, dt))
+        return np.ascontiguousarray(bits).reshape(arr.shape), list(arr.shape)
 
     def quant_matrix(self, base):
         """The quantized matrix `{base}.weight` as stored (src/checkpoint.rs:370-375)."""

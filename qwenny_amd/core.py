@@ -27,13 +27,14 @@ class Wt(IntEnum):
     I4Z = 3
     I4_S32 = 4
     I4Z_S32 = 5
+    BF16 = 6  # dense 16-bit weights kept bf16 (Wt::F16, which rounds them to f16)
 
     @property
     def has_zeros(self):
         return self in (Wt.I4Z, Wt.I4Z_S32)
 
     def bits(self):
-        return 8 if self is Wt.I8 else 4
+        return {Wt.I8: 8, Wt.BF16: 16}.get(self, 4)
 
 
 class Epi(IntEnum):
@@ -273,14 +274,28 @@ class Mat:
 
     @classmethod
     def new(cls, gemm, w_bf16, cols, silu=False, int8=True):
-        """Pack dense bf16 [rows][cols] requantized to int8 (src/cuda/core.rs:126-135). Dense 16-bit products are
-        not built here: int8=False raises."""
-        if not int8:
-            raise NotImplementedError("dense 16-bit products are outside this build (int8 requantization only)")
+        """Pack dense bf16 [rows][cols] (src/cuda/core.rs:126-135): requantized to int8 (Wt.I8), or with int8 False
+        kept 16-bit (Wt.BF16; the reference's Wt::F16 rounds to f16, here the bf16 values stay as they are)."""
         w = np.ascontiguousarray(w_bf16, np.uint16).reshape(-1, cols)
         h = P()
-        check(lib().qh_mat_dense_int8(gemm._ctx, _np_ptr(w), w.shape[0], cols, int(silu), ctypes.byref(h)))
+        fn = lib().qh_mat_dense_int8 if int8 else lib().qh_mat_dense
+        check(fn(gemm._ctx, _np_ptr(w), w.shape[0], cols, int(silu), ctypes.byref(h)))
         return cls(gemm, h)
+
+    @classmethod
+    def from_checkpoint(cls, gemm, ck, names, silu=False, int8=True):
+        """Matrices `names` (`.weight`) of a checkpoint with the same column count, stacked by rows
+        (src/cuda/core.rs:193-219 Mat::stack): stored quantized ones as Mat.stack takes them; else dense, requantized
+        to int8 when `int8` unless the checkpoint is pre-quantized (its 16-bit matrices stay 16-bit)."""
+        bases = [n[:-len(".weight")] for n in names if n.endswith(".weight")]
+        if len(bases) == len(names) and all(ck.is_quant(b) for b in bases):
+            return cls.stack(gemm, [ck.quant_matrix(b) for b in bases], silu, int8)
+        parts = [ck.bf16(n) for n in names]
+        cols = parts[0][1][1]
+        if any(shape[1] != cols for _, shape in parts):
+            raise ValueError(f"{names[0]}: stacking matrices of different column counts")
+        dense = np.concatenate([w.reshape(-1, cols) for w, _ in parts])
+        return cls.new(gemm, dense, cols, silu, int8 and not ck.prequantized())
 
     @classmethod
     def stack(cls, gemm, parts, silu=False, int8=True):
@@ -334,6 +349,24 @@ def unpack_rows(wt, rows, cols, codes, scales, zeros=None):
         check(lib().qh_unpack_row(int(wt), rows, cols, _np_ptr(codes), _np_ptr(scales), _np_ptr(zeros), p,
                                   _np_ptr(vals[p]), _np_ptr(sc[p]), _np_ptr(z[p])))
     return vals, sc, z
+
+
+def pack_dense_bf16(w_bf16, order):
+    """Dense bf16 rows `order` in the QH_WT_BF16 tile layout (src/cuda/core.rs:370-381, kept bf16) -> codes bytes."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    order = np.ascontiguousarray(order, np.uintp)
+    cb, _, _ = packed_sizes(Wt.BF16, order.size, w.shape[1])
+    codes = np.empty(cb, np.uint8)
+    check(lib().qh_pack_dense_bf16(_np_ptr(w), w.shape[0], w.shape[1], _np_ptr(order), order.size, _np_ptr(codes)))
+    return codes
+
+
+def unpack_rows_bf16(rows, cols, codes):
+    """The QH_WT_BF16 packer's inverse: bf16 bits [rows][cols] in packed row order."""
+    out = np.empty((rows, cols), np.uint16)
+    for p in range(rows):
+        check(lib().qh_unpack_row_bf16(rows, cols, _np_ptr(codes), p, _np_ptr(out[p])))
+    return out
 
 
 def pack_dense_int8(w_bf16, order):

@@ -124,7 +124,8 @@ static int mat_alloc(int wt, size_t rows, size_t cols, size_t valid, qh_mat** ou
     }
     size_t tiles = rows / TILE;
     size_t stage = (m->code_bytes + m->scale_bytes + m->zero_bytes) / tiles;
-    if (hipMalloc(&m->codes, m->code_bytes) != hipSuccess || hipMalloc(&m->scales, m->scale_bytes) != hipSuccess ||
+    if (hipMalloc(&m->codes, m->code_bytes) != hipSuccess ||
+        (m->scale_bytes && hipMalloc(&m->scales, m->scale_bytes) != hipSuccess) ||
         (m->zero_bytes && hipMalloc(&m->zeros, m->zero_bytes) != hipSuccess) ||
         hipHostMalloc((void**)&m->stage, stage, hipHostMallocDefault) != hipSuccess ||
         hipEventCreateWithFlags(&m->staged, hipEventDisableTiming) != hipSuccess) {
@@ -137,11 +138,12 @@ static int mat_alloc(int wt, size_t rows, size_t cols, size_t valid, qh_mat** ou
 
 extern "C" int qh_mat_upload(qh_ctx* ctx, int wt, size_t rows, size_t cols, const void* codes, const void* scales,
                              const void* zeros, size_t valid, qh_mat** out) {
-    if (!ctx || !codes || !scales || !out || (has_zeros(wt) && !zeros)) return fail(QH_EINVAL, "upload: null");
+    if (!ctx || !codes || (has_scales(wt) && !scales) || !out || (has_zeros(wt) && !zeros))
+        return fail(QH_EINVAL, "upload: null");
     qh_mat* m = nullptr;
     if (int e = mat_alloc(wt, rows, cols, valid, &m)) return e;
     if (hipMemcpy(m->codes, codes, m->code_bytes, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(m->scales, scales, m->scale_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+        (m->scale_bytes && hipMemcpy(m->scales, scales, m->scale_bytes, hipMemcpyHostToDevice) != hipSuccess) ||
         (m->zero_bytes && hipMemcpy(m->zeros, zeros, m->zero_bytes, hipMemcpyHostToDevice) != hipSuccess)) {
         mat_release(m);
         return fail(QH_EHIP, "upload of %zu x %zu failed", rows, cols);
@@ -225,6 +227,17 @@ extern "C" int qh_mat_dense_int8(qh_ctx* ctx, const uint16_t* bf16, size_t rows,
     return qh_mat_upload(ctx, QH_WT_I8, rows, cols, codes.data(), scales.data(), nullptr, rows, out);
 }
 
+extern "C" int qh_mat_dense(qh_ctx* ctx, const uint16_t* bf16, size_t rows, size_t cols, int silu, qh_mat** out) {
+    if (!ctx || !bf16 || !out) return fail(QH_EINVAL, "dense bf16: null");
+    size_t cb;
+    if (int e = qh_packed_sizes(QH_WT_BF16, rows, cols, &cb, nullptr, nullptr)) return e;
+    std::vector<size_t> order(rows);
+    if (int e = qh_row_order(rows, silu, order.data())) return e;
+    std::vector<uint8_t> codes(cb);
+    if (int e = qh_pack_dense_bf16(bf16, rows, cols, order.data(), rows, codes.data())) return e;
+    return qh_mat_upload(ctx, QH_WT_BF16, rows, cols, codes.data(), nullptr, nullptr, rows, out);
+}
+
 extern "C" int qh_mat_describe(const qh_mat* m, qh_mat_desc* out) {
     if (!m || !out) return fail(QH_EINVAL, "describe: null");
     *out = qh_mat_desc{m->wt, m->rows, m->cols, m->valid, m->code_bytes, m->scale_bytes, m->zero_bytes};
@@ -232,9 +245,9 @@ extern "C" int qh_mat_describe(const qh_mat* m, qh_mat_desc* out) {
 }
 
 extern "C" int qh_mat_download(const qh_mat* m, void* codes, void* scales, void* zeros) {
-    if (!m || !codes || !scales) return fail(QH_EINVAL, "download: null");
+    if (!m || !codes || (m->scale_bytes && !scales)) return fail(QH_EINVAL, "download: null");
     HIP_TRY(hipMemcpy(codes, m->codes, m->code_bytes, hipMemcpyDeviceToHost));
-    HIP_TRY(hipMemcpy(scales, m->scales, m->scale_bytes, hipMemcpyDeviceToHost));
+    if (m->scale_bytes) HIP_TRY(hipMemcpy(scales, m->scales, m->scale_bytes, hipMemcpyDeviceToHost));
     if (zeros && m->zero_bytes) HIP_TRY(hipMemcpy(zeros, m->zeros, m->zero_bytes, hipMemcpyDeviceToHost));
     return QH_OK;
 }
@@ -257,7 +270,8 @@ struct Partition {
 static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tokens, bool plain) {
     const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
     const int cols = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;  // wave columns over the tiles
-    const int ng = G % 4 == 0 ? 4 : 1;
+    // groups per wave: 4 (int4 and int8: 4 KiB or 8 KiB of a tile per wave), 1 for bf16 (4 KiB per group)
+    const int ng = !is_bf16(m->wt) && G % 4 == 0 ? 4 : 1;
     const int want_wt = ctx->skinny_tile_waves > 0 ? ctx->skinny_tile_waves : (tokens <= 2 ? 4 : 8);
     if (plain) {
         const int wt = std::max(1, std::min(want_wt, cols));
@@ -313,8 +327,9 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     l.codes = w->codes;
     l.scales = w->scales;
     l.zeros = (const uint16_t*)w->zeros;
-    l.fmt = (is_i8(w->wt) ? F_I8 | (w->per_channel ? F_PERCH : 0) : 0) | (has_zeros(w->wt) ? F_ZP : 0) |
-            (f32_scales(w->wt) ? F_S32 : 0);
+    l.fmt = is_bf16(w->wt) ? F_BF16
+                           : (is_i8(w->wt) ? F_I8 | (w->per_channel ? F_PERCH : 0) : 0) | (has_zeros(w->wt) ? F_ZP : 0) |
+                                 (f32_scales(w->wt) ? F_S32 : 0);
     l.rows = (int)w->rows;
     l.cols = (int)w->cols;
     l.valid = (int)w->valid;
@@ -355,7 +370,7 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
 extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros,
                             size_t block, const size_t* rows16) {
     if (!ctx || !m || !q || !zeros || !rows16) return fail(QH_EINVAL, "put block: null");
-    if (is_i8(m->wt) || q->bits != 4) return fail(QH_EINVAL, "put block: int4 matrices only");
+    if (is_i8(m->wt) || is_bf16(m->wt) || q->bits != 4) return fail(QH_EINVAL, "put block: int4 matrices only");
     if (q->cols != m->cols || (block + 1) * TILE > m->rows)
         return fail(QH_EINVAL, "block %zu of a matrix of %zu rows", block, m->rows);
     const size_t qgroups = q->cols / (size_t)q->group;

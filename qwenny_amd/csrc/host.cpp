@@ -4,6 +4,7 @@
 #include <stdarg.h>
 
 #include <algorithm>
+#include <cstring>
 #include <thread>
 #include <vector>
 
@@ -150,7 +151,7 @@ extern "C" int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_by
         return fail(QH_EINVAL, "%zu x %zu: rows must be a multiple of 16, columns of 128", rows, cols);
     size_t tiles = rows / TILE, blocks = tiles * (cols / QG), qd = tiles * quads(cols / QG);
     if (code_bytes) *code_bytes = blocks * block_bytes(wt);
-    if (scale_bytes) *scale_bytes = qd * TILE * 4 * (f32_scales(wt) ? 4 : 2);
+    if (scale_bytes) *scale_bytes = has_scales(wt) ? qd * TILE * 4 * (f32_scales(wt) ? 4 : 2) : 0;
     if (zero_bytes) *zero_bytes = has_zeros(wt) ? qd * TILE * 2 : 0;
     return QH_OK;
 }
@@ -204,7 +205,7 @@ extern "C" int qh_pack_quant(const qh_quant* q, const uint8_t* zeros, const size
                              void* codes, void* scales, void* zeros_out) {
     if (int e = check_quant(q)) return e;
     if (!order || !codes || !scales) return fail(QH_EINVAL, "pack: null buffer");
-    if (!valid_wt(wt) || is_i8(wt) != (q->bits == 8))
+    if (!valid_wt(wt) || is_bf16(wt) || is_i8(wt) != (q->bits == 8))
         return fail(QH_EINVAL, "pack: storage %d for %d-bit values", wt, q->bits);
     if (has_zeros(wt) && (!zeros || !zeros_out)) return fail(QH_EINVAL, "pack: zero points needed");
     if (q->group % QG || q->cols % QG || n == 0 || n % TILE)
@@ -227,6 +228,7 @@ extern "C" int qh_pack_quant(const qh_quant* q, const uint8_t* zeros, const size
 extern "C" int qh_unpack_row(int wt, size_t rows, size_t cols, const void* codes, const void* scales,
                              const void* zeros, size_t p, uint8_t* vals, float* sc, uint8_t* z) {
     if (int e = qh_packed_sizes(wt, rows, cols, nullptr, nullptr, nullptr)) return e;
+    if (is_bf16(wt)) return fail(QH_EINVAL, "unpack: dense bf16 rows unpack with qh_unpack_row_bf16");
     if (p >= rows || !codes || !scales || !vals || !sc || !z || (has_zeros(wt) && !zeros))
         return fail(QH_EINVAL, "unpack: row %zu of %zu or null buffer", p, rows);
     size_t G = cols / QG, t = p / TILE;
@@ -298,5 +300,40 @@ extern "C" int qh_pack_dense_int8(const uint16_t* bf16, size_t rows, size_t cols
             pack_tile(QH_WT_I8, cols, local, t, word, scale, zero, codes, scales, nullptr);
         }
     });
+    return QH_OK;
+}
+
+// Mat::new / pack, 16-bit branch (cuda/core.rs:127-135, :370-381): the reference stores f16 tiles; here the weights stay
+// bf16 (the checkpoint's own values, bit for bit) in the QH_WT_BF16 layout.
+extern "C" int qh_pack_dense_bf16(const uint16_t* bf16, size_t rows, size_t cols, const size_t* order, size_t n,
+                                  void* codes) {
+    if (!bf16 || !order || !codes) return fail(QH_EINVAL, "dense bf16: null buffer");
+    if (int e = qh_packed_sizes(QH_WT_BF16, n, cols, nullptr, nullptr, nullptr)) return e;
+    for (size_t i = 0; i < n; i++)
+        if (order[i] >= rows) return fail(QH_EINVAL, "dense bf16: row %zu of %zu", order[i], rows);
+    const size_t G = cols / QG;
+    uint16_t* out = (uint16_t*)codes;
+    parallel(n / TILE, [&](size_t lo, size_t hi) {
+        for (size_t t = lo; t < hi; t++)
+            for (size_t g = 0; g < G; g++)
+                for (int j = 0; j < 4; j++)
+                    for (int l = 0; l < LANES; l++) {
+                        const uint16_t* src = bf16 + order[t * TILE + l % 16] * cols + g * QG + 32 * j + 8 * (l / 16);
+                        std::memcpy(out + (((t * G + g) * 4 + j) * LANES + l) * 8, src, 16);
+                    }
+    });
+    return QH_OK;
+}
+
+// The inverse for one packed row p of a QH_WT_BF16 matrix: its bf16 values into out[cols].
+extern "C" int qh_unpack_row_bf16(size_t rows, size_t cols, const void* codes, size_t p, uint16_t* out) {
+    if (int e = qh_packed_sizes(QH_WT_BF16, rows, cols, nullptr, nullptr, nullptr)) return e;
+    if (p >= rows || !codes || !out) return fail(QH_EINVAL, "unpack bf16: row %zu of %zu or null buffer", p, rows);
+    const size_t G = cols / QG, t = p / TILE;
+    const uint16_t* in = (const uint16_t*)codes;
+    for (size_t g = 0; g < G; g++)
+        for (int j = 0; j < 4; j++)
+            for (int l = (int)(p % TILE); l < LANES; l += 16)
+                std::memcpy(out + g * QG + 32 * j + 8 * (l / 16), in + (((t * G + g) * 4 + j) * LANES + l) * 8, 16);
     return QH_OK;
 }

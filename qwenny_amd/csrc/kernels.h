@@ -12,6 +12,7 @@ enum {
     F_ZP = 2,     // int4 with zero points
     F_S32 = 4,    // f32 scales (else bf16)
     F_PERCH = 8,  // int8 with one scale per row: exact integer weights, the row's scale after the sum
+    F_BF16 = 16,  // dense bf16 weights (4 KiB blocks, no scales): B fragments as loaded
 };
 
 struct Launch {

@@ -155,7 +155,7 @@ __device__ void argmax_finish(const Launch& a) {
 // Words of a (tile, group) code block per lane (16 bytes each).
 template <int F>
 struct CodeWords {
-    static constexpr int N = (F & F_I8) ? 2 : 1;
+    static constexpr int N = (F & F_BF16) ? 4 : (F & F_I8) ? 2 : 1;
 };
 
 // The scale and zero point of row r of `tile`, group g (G groups; layout.h scale_idx / zero_idx)
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
         uint32_t zraw[T];
         u32x4 code[NG][T][CW];
 #pragma unroll
-        for (int t = 0; t < T; t++) {
+        for (int t = 0; t < T && !(F & F_BF16); t++) {
             const size_t si = scale_idx(tt[t], G, gw, l16);
             if (NG == 4) {
                 if (F & F_S32) {
@@ -282,18 +282,25 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
             for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow + 32 * j);
             f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
+            for (int j = 0; j < 4 && !(F & F_BF16); j++) xsum = mfma(xa[j], ones, xsum);
 #pragma unroll
             for (int t = 0; t < T; t++) {
                 f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     bf16x8 b;
-                    if (F & F_I8)
+                    if (F & F_BF16)
+                        b = __builtin_bit_cast(bf16x8, code[gi][t][j]);
+                    else if (F & F_I8)
                         b = i8_biased(code[gi][t][j >> 1][2 * (j & 1)], code[gi][t][j >> 1][2 * (j & 1) + 1]);
                     else
                         b = i4_biased(code[gi][t][0][j], mask, magic);
                     d = mfma(xa[j], b, d);
+                }
+                if (F & F_BF16) {  // the weights themselves: no scale, no zero point
+#pragma unroll
+                    for (int r = 0; r < NR; r++) acc[t][r] += d[r];
+                    continue;
                 }
                 const int g = gw + gi;
                 // the group's scale from the raw scale words: f32 one per word; bf16 two per word (NG == 4) or one
@@ -510,7 +517,10 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             for (int pc = 0; pc < 2; pc++)
 #pragma unroll
                 for (int h = 0; h < CW; h++) f.c[t][pc][h] = *(const u32x4*)(cb + cg[t] + (h * 64 + 32 * pc) * 16);
-            if (F & F_PERCH) {
+            if (F & F_BF16) {
+                f.s[t] = 1.0f;  // the weights themselves
+                f.off[t] = 0.0f;
+            } else if (F & F_PERCH) {
                 f.s[t] = 1.0f;  // exact integers q = stored - 128; the row scale comes after the sum
                 f.off[t] = -128.0f;
             } else {
@@ -527,6 +537,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // B fragment of output block t for k16 step kk (0..7) of the group
     auto dequant = [&](const WFrag& f, int t, int kk) -> bf16x8 {
         const int pc = kk & 1, i = kk >> 1;
+        if (F & F_BF16) return __builtin_bit_cast(bf16x8, f.c[t][pc][i]);  // step kk's piece as stored
         if (F & F_I8)  // int8: word pair (2e, 2e + 1) of half h, for k32 step i = 2h + e
             return i8_scaled(f.c[t][pc][i >> 1][2 * (i & 1)], f.c[t][pc][i >> 1][2 * (i & 1) + 1], f.s[t], f.off[t]);
         return i4_scaled(f.c[t][pc][0][i], f.s[t], f.off[t]);
@@ -726,7 +737,10 @@ static hipError_t skinny_ng(const Launch& l) {
 
 template <int F, int EPI, int NR>
 static hipError_t skinny_nr(const Launch& l) {
-    return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4>(l) : skinny_ng<F, EPI, NR, 1>(l);
+    if constexpr ((F & F_BF16) != 0)
+        return skinny_ng<F, EPI, NR, 1>(l);  // one 4 KiB group of a tile per wave
+    else
+        return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4>(l) : skinny_ng<F, EPI, NR, 1>(l);
 }
 
 template <int F, int EPI>
@@ -842,6 +856,7 @@ hipError_t launch(const Launch& l) {
         case F_ZP | F_S32: return launch_fmt<F_ZP | F_S32>(l);
         case F_I8 | F_S32: return launch_fmt<F_I8 | F_S32>(l);
         case F_I8 | F_S32 | F_PERCH: return launch_fmt<F_I8 | F_S32 | F_PERCH>(l);
+        case F_BF16: return launch_fmt<F_BF16>(l);
         default: return hipErrorInvalidValue;
     }
 }

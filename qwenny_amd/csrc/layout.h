@@ -15,6 +15,8 @@
 //    Stored values are the checkpoint's unsigned codes (q + 8 of a symmetric value).
 //  int8 (QH_WT_I8): 2048 B per block = [h][lane][w] u32, h = 0, 1: words w = 2e + i, step j = 2h + e, column bytes
 //    4i + 0..3 in byte order; stored values q + 128.
+//  bf16 (QH_WT_BF16, dense 16-bit weights): 4096 B per block = [j][lane] 16 bytes, the lane's 8 columns of step j as
+//    bf16 in column order, so that each 16-byte piece is a B fragment as loaded. No scales or zero points.
 //
 // Scales: per tile, per quad of 4 groups (the group count padded up to a multiple of 4), per row of the tile, the
 // quad's 4 groups: [t][g / 4][16][g % 4], so that one 8-byte load gives a row the scales of 4 consecutive groups.
@@ -33,12 +35,14 @@ constexpr int LANES = 64;  // wavefront size
 
 // storage properties (enum qh_wt values)
 constexpr bool is_i8(int wt) { return wt == 1; }
+constexpr bool is_bf16(int wt) { return wt == 6; }
 constexpr bool has_zeros(int wt) { return wt == 3 || wt == 5; }
+constexpr bool has_scales(int wt) { return !is_bf16(wt); }
 constexpr bool f32_scales(int wt) { return wt == 1 || wt == 4 || wt == 5; }
-constexpr bool valid_wt(int wt) { return wt >= 1 && wt <= 5; }
+constexpr bool valid_wt(int wt) { return wt >= 1 && wt <= 6; }
 
 // bytes of one (tile, group) code block
-constexpr size_t block_bytes(int wt) { return is_i8(wt) ? 2048 : 1024; }
+constexpr size_t block_bytes(int wt) { return is_bf16(wt) ? 4096 : is_i8(wt) ? 2048 : 1024; }
 
 // quads of 4 groups (scale and zero-point blocks) for G groups
 constexpr size_t quads(size_t G) { return (G + 3) / 4; }

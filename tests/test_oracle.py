@@ -238,3 +238,30 @@ def test_argmax_keys():
     v = np.array([-np.inf, -3.0, -1e-30, -0.0, 0.0, 1e-30, 2.0, np.inf], np.float32)
     o = oracle.ordered(v)
     assert (np.diff(o.astype(np.int64)) > 0).all()
+
+
+# ---- the dense 16-bit product (src/cuda/core.rs:370-381, kernels/gemm.cuh:120-212) ------------------------------
+
+
+def test_dense_f64_closed_forms():
+    """Small integers are exact in bf16, f16 and f64: the product is the integer matrix product, by hand; a one-hot x
+    selects a weight column."""
+    w = np.array([[1, -2, 3, 0], [4, 5, -6, 7]], np.float32)
+    x = np.array([[2, 1, 0, -1], [0, 0, 1, 0]], np.float32)
+    want = np.array([[0, 6], [3, -6]], np.float64)  # rows of x against rows of w
+    for f16 in (False, True):
+        assert np.array_equal(oracle.dense_f64(f32_to_bf16(w), f32_to_bf16(x), f16), want)
+
+
+def test_dense_f64_f16_storage():
+    """The reference's f16 storage changes a bf16 weight only outside f16's normal range: below 2^-14 it becomes an f16
+    subnormal (a multiple of 2^-24, nearest even), above 65504 infinity; in range bf16 values are exact in f16."""
+    w = f32_to_bf16(np.array([[1.0e-6], [3.140625], [-65536.0], [0.0078125]], np.float32))  # 4 rows, 1 column
+    x = f32_to_bf16(np.ones((1, 1), np.float32))
+    exact = oracle.dense_f64(w, x)[0]
+    ref = oracle.dense_f64(w, x, f16_weights=True)[0]
+    wf = bf16_to_f32(w)[:, 0]
+    assert np.array_equal(exact, wf.astype(np.float64))
+    assert ref[0] == round(float(wf[0]) / 2.0 ** -24) * 2.0 ** -24 and ref[0] != exact[0]
+    assert ref[1] == exact[1] and ref[3] == exact[3]
+    assert ref[2] == -np.inf

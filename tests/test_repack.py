@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 
 import oracle
-from qwenny_amd import Wt, pack_dense_int8, pack_quant, row_order, unpack_rows
+from qwenny_amd import Wt, pack_dense_bf16, pack_dense_int8, pack_quant, packed_sizes, row_order, unpack_rows, \
+    unpack_rows_bf16
 from qwenny_amd.checkpoint import quant_from_packed
 from qwenny_amd.core import Quant
 from qwenny_amd.synth import bf16_to_f32, f32_to_bf16
@@ -89,6 +90,28 @@ def test_dense_int8_matches_oracle():
     vals, sc, zz = unpack_rows(Wt.I8, 48, 384, codes, scales)
     ovals, osc = oracle.requant_int8(w)
     assert np.array_equal(vals, ovals[order]) and np.array_equal(sc, osc[order]) and (zz == 128).all()
+
+
+@pytest.mark.parametrize("silu", [False, True])
+def test_dense_bf16_roundtrip(silu):
+    """Dense 16-bit matrices keep their bf16 values bit for bit through the tile layout, in row_order."""
+    w = f32_to_bf16(np.random.default_rng(8).standard_normal((96, 384)).astype(np.float32))
+    order = row_order(96, silu)
+    codes = pack_dense_bf16(w, order)
+    assert codes.size == packed_sizes(Wt.BF16, 96, 384)[0] == 96 * 384 * 2
+    assert packed_sizes(Wt.BF16, 96, 384)[1:] == (0, 0)
+    assert np.array_equal(unpack_rows_bf16(96, 384, codes), w[order])
+
+
+def test_dense_bf16_layout():
+    """The documented block order: block (tile, group) = [step j][lane] 16 bytes, lane l holding row l % 16 and
+    columns 32 j + 8 (l / 16) + 0..7 of the group, so each piece is a B fragment as loaded."""
+    rows, cols = 32, 256
+    w = np.arange(rows * cols, dtype=np.uint16).reshape(rows, cols)  # value = 256 row + column
+    pieces = pack_dense_bf16(w, np.arange(rows)).view(np.uint16).reshape(rows // 16, cols // 128, 4, 64, 8)
+    for t, g, j, l in [(0, 0, 0, 0), (0, 0, 0, 17), (0, 1, 3, 63), (1, 1, 2, 5)]:
+        r, c0 = 16 * t + l % 16, 128 * g + 32 * j + 8 * (l // 16)
+        assert np.array_equal(pieces[t, g, j, l], w[r, c0:c0 + 8])
 
 
 # ---- the product's host functions vs the oracle -----------------------------------------------------------------
