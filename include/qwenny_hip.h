@@ -185,6 +185,14 @@ int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ld
 int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros, size_t block,
                  const size_t* rows16);
 
+/* The trainer's dequant (kernels/qwen_train.cu:84-103, called by src/cuda/qwen/train.rs:490-520): rows
+ * [r0, r0 + n) of a quantized matrix in the checkpoint's layout (q [rows][words] u32, value c in word c * bits / 32
+ * from the low bits; scales f32 and zero points u8 per (row, group)) into dense rows out [n][cols] on `stream`:
+ * w = (q - zero) * scale in f32, stored bf16 (nearest even; out_f32 = 0) or f32. All pointers are device addresses,
+ * q and out 16-byte aligned; group a multiple of 32 / bits. Launch only. */
+int qh_dequant(void* stream, const uint32_t* q, const float* scales, const uint8_t* zeros, size_t rows, size_t words,
+               size_t cols, int group, int bits, size_t r0, size_t n, void* out, int out_f32);
+
 #ifdef __cplusplus
 }
 #endif

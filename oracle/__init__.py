@@ -139,6 +139,25 @@ def dense_f64(w_bf16, x_bf16, f16_weights=False):
     return x.astype(np.float64) @ w.astype(np.float64).T
 
 
+def dequant_rows(bits, group, q, scales, zeros, r0, n, out_f32=False):
+    """The trainer's dequant (kernels/qwen_train.cu:84-103): rows [r0, r0 + n) of q (u32 [rows][words], value c in
+    word c * bits / 32 from the low bits) as ((float) q - zero) * scale in f32 per (row, group), then bf16 bits
+    (nearest even, the bf16 build's to_act) or f32."""
+    per = 32 // bits
+    q = np.asarray(q, np.uint32)[r0:r0 + n]
+    cols = q.shape[1] * per
+    c = np.arange(cols)
+    vals = ((q[:, c // per] >> ((c % per) * bits).astype(np.uint32)) & ((1 << bits) - 1)).astype(np.float32)
+    g = cols // group
+    s = np.asarray(scales, np.float32).reshape(-1, g)[r0:r0 + n][:, c // group]
+    z = np.asarray(zeros, np.uint8).reshape(-1, g)[r0:r0 + n][:, c // group].astype(np.float32)
+    w = (vals - z) * s  # f32: the difference is exact, the product rounds once
+    if out_f32:
+        return w
+    u = w.view(np.uint32).astype(np.uint64)  # round to nearest even (no NaN arises from finite inputs)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
 # ---- epilogues (numpy restatements) ---------------------------------------------------------------------------
 
 

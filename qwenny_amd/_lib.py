@@ -42,6 +42,7 @@ SIGNATURES = {
     "qh_mat_quant_rows": (I, [P, ctypes.POINTER(QuantC), P, P, S, S, ctypes.POINTER(P)]),
     "qh_mat_dense_int8": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
     "qh_mat_dense": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
+    "qh_dequant": (I, [P, P, P, P, S, S, S, I, I, S, S, P, I]),
     "qh_pack_dense_bf16": (I, [P, S, S, P, S, P]),
     "qh_unpack_row_bf16": (I, [S, S, P, S, P]),
     "qh_mat_free": (None, [P]),

@@ -351,6 +351,14 @@ def unpack_rows(wt, rows, cols, codes, scales, zeros=None):
     return vals, sc, z
 
 
+def dequant(stream, q, scales, zeros, rows, words, cols, group, bits, r0, n, out, out_f32=False):
+    """The trainer's dequant (kernels/qwen_train.cu:84-103): rows [r0, r0 + n) of a quantized matrix in the
+    checkpoint's layout, all device buffers (q u32 [rows][words], scales f32 and zeros u8 per (row, group)), into
+    dense rows `out` [n][cols], bf16 or f32, on `stream`."""
+    check(lib().qh_dequant(_stream(stream), _ptr(q), _ptr(scales), _ptr(zeros), rows, words, cols, group, bits, r0,
+                           n, _ptr(out), int(out_f32)))
+
+
 def pack_dense_bf16(w_bf16, order):
     """Dense bf16 rows `order` in the QH_WT_BF16 tile layout (src/cuda/core.rs:370-381, kept bf16) -> codes bytes."""
     w = np.ascontiguousarray(w_bf16, np.uint16)

@@ -265,3 +265,39 @@ def test_dense_f64_f16_storage():
     assert ref[0] == round(float(wf[0]) / 2.0 ** -24) * 2.0 ** -24 and ref[0] != exact[0]
     assert ref[1] == exact[1] and ref[3] == exact[3]
     assert ref[2] == -np.inf
+
+
+# ---- the trainer's dequant (kernels/qwen_train.cu:84-103) -------------------------------------------------------
+
+
+def test_dequant_rows_known_words():
+    """Hand-packed words: int4 values 0..15 along a row (low nibble first) with zero point 8 and scale 0.5; int8 bytes
+    1, 0, 255, 128 with zero point 128 and scale 2. Every result is exact in bf16."""
+    q4 = np.array([[0x76543210, 0xFEDCBA98] * 8], np.uint32)  # 128 columns: 0..15 repeated
+    got = oracle.dequant_rows(4, 128, q4, np.array([0.5], np.float32), np.array([8], np.uint8), 0, 1)
+    want = (np.tile(np.arange(16), 8) - 8) * 0.5
+    assert np.array_equal(bf16_to_f32(got)[0], want.astype(np.float32))
+    q8 = np.array([[0x80FF0001]], np.uint32)
+    got = oracle.dequant_rows(8, 4, q8, np.array([2.0], np.float32), np.array([128], np.uint8), 0, 1, out_f32=True)
+    assert np.array_equal(got[0], np.array([-254, -256, 254, 0], np.float32))
+
+
+def test_dequant_rows_rounding_and_rows():
+    """The f32 product rounds once, then to bf16 nearest even, checked against torch's bf16 conversion; rows r0..r0+n
+    of the matrix and per-group scales and zero points."""
+    import torch
+
+    rng = np.random.default_rng(12)
+    rows, cols, group = 6, 256, 128
+    q = rng.integers(0, 2**32, (rows, cols // 8), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(0.001, 0.05, rows * 2).astype(np.float32)
+    z = rng.integers(0, 16, rows * 2).astype(np.uint8)
+    got32 = oracle.dequant_rows(4, group, q, s, z, 2, 3, out_f32=True)
+    got16 = oracle.dequant_rows(4, group, q, s, z, 2, 3)
+    for i, r in enumerate(range(2, 5)):
+        for c in (0, 1, 127, 128, 255):
+            v = (q[r, c // 8] >> (4 * (c % 8))) & 15
+            w = np.float32(np.float32(int(v) - int(z[r * 2 + c // 128])) * s[r * 2 + c // 128])
+            assert got32[i, c] == w
+    want16 = torch.from_numpy(got32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got16, want16)
