@@ -231,6 +231,88 @@ def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
     print(json.dumps(res))
 
 
+def dense_weights(seed, n, k):
+    """Synthetic dense bf16 weights [n][k] ~ N(0, 0.05^2)."""
+    from qwenny_amd.synth import f32_to_bf16
+
+    rng = np.random.default_rng(seed)
+    return f32_to_bf16((rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.05)))
+
+
+def dense_lines(gemm, args):
+    """The dense 16-bit products (Wt::F16 rows, kept bf16): M = 1 over (5120, 17408) and (17408, 5120) in 4 device
+    copies (HBM GB/s), and M = 2048 on (5120, 17408) (TFLOP/s) beside torch's bf16 product of the same shape."""
+    import torch
+
+    from qwenny_amd import Epi, Mat
+
+    shapes = [(5120, 17408), (17408, 5120)]
+    mats = []
+    for i, (k, n) in enumerate(shapes):
+        w = dense_weights(400 + i, n, k)
+        mats.append([Mat.new(gemm, w, k, int8=False) for _ in range(4)])
+        del w
+    st = Step(gemm, 1, 17408)
+    for c in range(4):
+        for m, (k, n) in zip(mats, shapes):
+            st.add(m[c], Epi.Plain, k * n * 2 + 2 * k + 2 * n, 2 * k * n)
+    ms = time_step(st, args.steps, args.warmup, not args.no_graph)
+    out = {"bf16_dense_m1_GBps": round(st.bytes() / (ms * 1e-3) / 1e9, 1)}
+    k, n = shapes[0]
+    pst = Step(gemm, 2048, k)
+    pst.add(mats[0][0], Epi.Plain, k * n * 2 + 2048 * (k + n) * 2, 2 * 2048 * k * n)
+    msp = time_step(pst, max(10, args.steps // 10), 3, False)
+    out["bf16_dense_prefill_m2048_TFLOPs"] = round(pst.flops() / (msp * 1e-3) / 1e12, 1)
+    a = torch.randn(2048, k, device="cuda").to(torch.bfloat16)
+    b = torch.randn(n, k, device="cuda").to(torch.bfloat16)
+    for _ in range(3):
+        a @ b.t()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(10, args.steps // 10)
+    t0.record()
+    for _ in range(reps):
+        a @ b.t()
+    t1.record()
+    torch.cuda.synchronize()
+    out["torch_bf16_prefill_m2048_TFLOPs"] = round(2 * 2048 * k * n / (t0.elapsed_time(t1) / reps * 1e-3) / 1e12, 1)
+    print(f"# dense bf16 M=1: {ms:.4f} ms/step, {out['bf16_dense_m1_GBps']} GB/s; M=2048 (5120x17408): "
+          f"{out['bf16_dense_prefill_m2048_TFLOPs']} TFLOP/s (torch {out['torch_bf16_prefill_m2048_TFLOPs']})",
+          file=sys.stderr, flush=True)
+    return out
+
+
+def dequant_line(args):
+    """The trainer's dequant of a whole (5120, 17408) int4 group-128 matrix in the checkpoint layout to bf16 rows,
+    rotating 4 device copies of the input: HBM GB/s over words + f32 scales + u8 zeros read and bf16 written."""
+    import torch
+
+    from qwenny_amd import dequant
+
+    k, n = 5120, 17408
+    q = quant(500, "i4", k, n)
+    z = q.zero_points()
+    ins = [(torch.from_numpy(q.q).cuda(), torch.from_numpy(q.scales).cuda(), torch.from_numpy(z).cuda())
+           for _ in range(4)]
+    out = torch.empty((n, k), dtype=torch.int16, device="cuda")
+    words = q.q.shape[1]
+    run = lambda i: dequant(None, ins[i][0], ins[i][1], ins[i][2], n, words, k, 128, 4, 0, n, out)
+    for i in range(4):
+        run(i)
+    torch.cuda.synchronize()
+    reps = max(20, args.steps // 5)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(reps):
+        run(i % 4)
+    t1.record()
+    torch.cuda.synchronize()
+    s = t0.elapsed_time(t1) / reps * 1e-3
+    nbytes = n * words * 4 + q.scales.size * 4 + z.size + n * k * 2
+    gbs = round(nbytes / s / 1e9, 1)
+    print(f"# dequant (5120, 17408) int4 -> bf16: {s * 1e6:.1f} us, {gbs} GB/s", file=sys.stderr, flush=True)
+    return {"dequant_i4_to_bf16_GBps": gbs}
+
+
 def summarize_clock(pmc_dir, min_ns=50000):
     """Per kernel (name, grid) of a rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: mean duration, the
     clock it ran at (GRBM_GUI_ACTIVE sums the 8 XCDs' cycles) and the fraction of cycles each SIMD's MFMA unit was busy
@@ -268,7 +350,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8")
+    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -297,7 +379,7 @@ def main():
 
     torch.cuda.init()
     gemm = Gemm.load(0)
-    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8"}
+    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8", "dense", "dequant"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
@@ -376,6 +458,10 @@ def main():
         ms8 = time_step(st, args.steps, args.warmup, not args.no_graph)
         extra["int8_m1_GBps"] = round(st.bytes() / (ms8 * 1e-3) / 1e9, 1)
         print(f"# int8 M=1: {ms8:.4f} ms/step, {extra['int8_m1_GBps']} GB/s", file=sys.stderr, flush=True)
+    if "dense" in only:
+        extra.update(dense_lines(gemm, args))
+    if "dequant" in only:
+        extra.update(dequant_line(args))
 
     line = {
         "metric": "int4 GEMM HBM GB/s (% of 8 TB/s) at M=1/5; TFLOP/s (% bf16 MFMA peak) at M=2048",

@@ -189,7 +189,7 @@ int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const 
  * [r0, r0 + n) of a quantized matrix in the checkpoint's layout (q [rows][words] u32, value c in word c * bits / 32
  * from the low bits; scales f32 and zero points u8 per (row, group)) into dense rows out [n][cols] on `stream`:
  * w = (q - zero) * scale in f32, stored bf16 (nearest even; out_f32 = 0) or f32. All pointers are device addresses,
- * q and out 16-byte aligned; group a multiple of 32 / bits. Launch only. */
+ * q 4-byte and out 16-byte aligned; group a multiple of 32 / bits. Launch only. */
 int qh_dequant(void* stream, const uint32_t* q, const float* scales, const uint8_t* zeros, size_t rows, size_t words,
                size_t cols, int group, int bits, size_t r0, size_t n, void* out, int out_f32);
 
