@@ -193,6 +193,15 @@ int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const 
 int qh_dequant(void* stream, const uint32_t* q, const float* scales, const uint8_t* zeros, size_t rows, size_t words,
                size_t cols, int group, int bits, size_t r0, size_t n, void* out, int out_f32);
 
+/* Consumers of the plain products' partials x [splits][n][.] f32 (device pointers, 16-byte aligned), on `stream`:
+ * sum_parts (kernels/qwen.cu:141-143): y [n][ld] = sum over s of x[s] (ld a multiple of 4);
+ * add_rmsnorm (kernels/qwen.cu:57-80), the residual step: h [n][hidden] += sum over s of x[s] (h + x[0] first, then
+ * x[1], ..), then y [n][hidden] bf16 = w_next * h / sqrt(mean(h^2) + eps) (hidden a multiple of 4). The sums are
+ * those of the reference, in its order. Launch only. */
+int qh_sum_parts(void* stream, const float* x, int splits, size_t n, size_t ld, float* y);
+int qh_add_rmsnorm(void* stream, float* h, const float* x, int splits, size_t n, size_t hidden, const float* w_next,
+                   void* y_bf16, float eps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,6 +158,28 @@ def dequant_rows(bits, group, q, scales, zeros, r0, n, out_f32=False):
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
+def sum_parts(x, splits):
+    """kernels/qwen.cu:141-143 (part_sum, kernels/common.cuh:66-70): the partials x [splits][n][ld] summed in f32 from
+    0, split 0 first."""
+    x = np.asarray(x, np.float32)
+    v = np.zeros(x.shape[1:], np.float32)
+    for s in range(splits):
+        v = v + x[s]
+    return v
+
+
+def add_rmsnorm(h, x, splits, w_next, eps):
+    """kernels/qwen.cu:57-80: h + x[0] + x[1] + .. in f32 (that order), then w * h / sqrt(mean(h^2) + eps) in f64;
+    returns (new h f32, y f64)."""
+    v = np.asarray(h, np.float32).copy()
+    x = np.asarray(x, np.float32)
+    for s in range(splits):
+        v = v + x[s]
+    d = v.astype(np.float64)
+    r = 1.0 / np.sqrt(np.mean(d * d, axis=-1, keepdims=True) + eps)
+    return v, np.asarray(w_next, np.float64) * (d * r)
+
+
 # ---- epilogues (numpy restatements) ---------------------------------------------------------------------------
 
 

@@ -43,6 +43,8 @@ SIGNATURES = {
     "qh_mat_dense_int8": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
     "qh_mat_dense": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
     "qh_dequant": (I, [P, P, P, P, S, S, S, I, I, S, S, P, I]),
+    "qh_sum_parts": (I, [P, P, I, S, S, P]),
+    "qh_add_rmsnorm": (I, [P, P, P, I, S, S, P, P, ctypes.c_float]),
     "qh_pack_dense_bf16": (I, [P, S, S, P, S, P]),
     "qh_unpack_row_bf16": (I, [S, S, P, S, P]),
     "qh_mat_free": (None, [P]),

@@ -359,6 +359,17 @@ def dequant(stream, q, scales, zeros, rows, words, cols, group, bits, r0, n, out
                            n, _ptr(out), int(out_f32)))
 
 
+def sum_parts(stream, x, splits, n, ld, y):
+    """y [n][ld] = the sum of a plain product's `splits` partials x [splits][n][ld] (kernels/qwen.cu:141-143)."""
+    check(lib().qh_sum_parts(_stream(stream), _ptr(x), splits, n, ld, _ptr(y)))
+
+
+def add_rmsnorm(stream, h, x, splits, n, hidden, w_next, y, eps=1e-6):
+    """The residual step after a plain product (kernels/qwen.cu:57-80): h [n][hidden] += the sum of the partials x,
+    then y [n][hidden] bf16 = w_next * h / rms(h)."""
+    check(lib().qh_add_rmsnorm(_stream(stream), _ptr(h), _ptr(x), splits, n, hidden, _ptr(w_next), _ptr(y), eps))
+
+
 def pack_dense_bf16(w_bf16, order):
     """Dense bf16 rows `order` in the QH_WT_BF16 tile layout (src/cuda/core.rs:370-381, kept bf16) -> codes bytes."""
     w = np.ascontiguousarray(w_bf16, np.uint16)

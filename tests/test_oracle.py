@@ -301,3 +301,28 @@ def test_dequant_rows_rounding_and_rows():
             assert got32[i, c] == w
     want16 = torch.from_numpy(got32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got16, want16)
+
+
+# ---- the partials consumers (kernels/qwen.cu:57-80, :141-143) ----------------------------------------------------
+
+
+def test_sum_parts_order_and_exactness():
+    """Small integers sum exactly in any order; a large-magnitude case fixes the reference's order, (0 + x0) + x1 + x2:
+    1e8 + 1 - 1e8 gives 0 in f32 (the 1 is lost), the other orders would not all agree."""
+    x = np.array([[[1.0, 2.0]], [[3.0, -4.0]], [[5.0, 6.0]]], np.float32)
+    assert np.array_equal(oracle.sum_parts(x, 3), np.array([[9.0, 4.0]], np.float32))
+    y = np.array([[[1e8]], [[1.0]], [[-1e8]]], np.float32)
+    assert oracle.sum_parts(y, 3)[0, 0] == 0.0
+    assert oracle.sum_parts(y, 2)[0, 0] == np.float32(1e8)
+
+
+def test_add_rmsnorm_closed_form():
+    """h = (3, 4) with no partials: mean(h^2) = 12.5, so y = w h / sqrt(12.5 + eps); the partials add before the norm."""
+    h = np.array([[3.0, 4.0]], np.float32)
+    w = np.array([2.0, 0.5], np.float32)
+    hn, y = oracle.add_rmsnorm(h, np.zeros((1, 1, 2), np.float32), 1, w, 1e-6)
+    assert np.array_equal(hn, h)
+    assert np.allclose(y, [[2 * 3 / np.sqrt(12.5 + 1e-6), 0.5 * 4 / np.sqrt(12.5 + 1e-6)]], rtol=1e-12)
+    hn, y = oracle.add_rmsnorm(np.zeros((1, 2), np.float32), np.array([[[1.0, 2.0]], [[2.0, 2.0]]], np.float32), 2,
+                               w, 0.0)
+    assert np.array_equal(hn, h) and np.allclose(y, [[2 * 3 / np.sqrt(12.5), 0.5 * 4 / np.sqrt(12.5)]], rtol=1e-12)
