@@ -27,6 +27,8 @@ namespace qh {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Kernel format F: bit flags of the storage (kernels.h F_*).
 
@@ -51,13 +53,12 @@ __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >
 
 // int8 words (columns 0..3, 4..7; stored q + 128) -> bf16 (128 + q), exact (integers below 256)
 __device__ __forceinline__ bf16x8 i8_biased(uint32_t a, uint32_t b) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        r[i] = (__bf16)byte_f(a, i);
-        r[4 + i] = (__bf16)byte_f(b, i);
-    }
-    return r;
+    auto pair = [](uint32_t v, int b0) {  // one v_cvt_pk_bf16_f32 per pair
+        const f32x2 f = {byte_f(v, b0), byte_f(v, b0 + 1)};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    };
+    const u32x4 r = {pair(a, 0), pair(a, 2), pair(b, 0), pair(b, 2)};
+    return __builtin_bit_cast(bf16x8, r);
 }
 
 // int4 word -> bf16 of (q - z) s = q s + off, in f32 then rounded once
@@ -67,26 +68,22 @@ __device__ __forceinline__ bf16x8 i4_scaled(uint32_t w, float s, float off) {
     // byte-to-float conversions (v_cvt_f32_ubyte0..3)
     asm("" : "+v"(lo));
     asm("" : "+v"(hi));
-    bf16x8 r;
-    r[0] = (__bf16)__builtin_fmaf(byte_f(lo, 0), s, off);
-    r[1] = (__bf16)__builtin_fmaf(byte_f(lo, 2), s, off);
-    r[2] = (__bf16)__builtin_fmaf(byte_f(hi, 0), s, off);
-    r[3] = (__bf16)__builtin_fmaf(byte_f(hi, 2), s, off);
-    r[4] = (__bf16)__builtin_fmaf(byte_f(lo, 1), s, off);
-    r[5] = (__bf16)__builtin_fmaf(byte_f(lo, 3), s, off);
-    r[6] = (__bf16)__builtin_fmaf(byte_f(hi, 1), s, off);
-    r[7] = (__bf16)__builtin_fmaf(byte_f(hi, 3), s, off);
-    return r;
+    // each bf16 pair is one two-wide conversion (v_cvt_pk_bf16_f32), so no halves are spliced afterwards
+    auto pair = [&](uint32_t v, int b0, int b1) {
+        const f32x2 f = {__builtin_fmaf(byte_f(v, b0), s, off), __builtin_fmaf(byte_f(v, b1), s, off)};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    };
+    const u32x4 r = {pair(lo, 0, 2), pair(hi, 0, 2), pair(lo, 1, 3), pair(hi, 1, 3)};
+    return __builtin_bit_cast(bf16x8, r);
 }
 
 __device__ __forceinline__ bf16x8 i8_scaled(uint32_t a, uint32_t b, float s, float off) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        r[i] = (__bf16)__builtin_fmaf(byte_f(a, i), s, off);
-        r[4 + i] = (__bf16)__builtin_fmaf(byte_f(b, i), s, off);
-    }
-    return r;
+    auto pair = [&](uint32_t v, int b0) {  // one v_cvt_pk_bf16_f32 per pair, as i4_scaled
+        const f32x2 f = {__builtin_fmaf(byte_f(v, b0), s, off), __builtin_fmaf(byte_f(v, b0 + 1), s, off)};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    };
+    const u32x4 r = {pair(a, 0), pair(a, 2), pair(b, 0), pair(b, 2)};
+    return __builtin_bit_cast(bf16x8, r);
 }
 
 __device__ __forceinline__ float bf16_bits_f(uint32_t b) { return __uint_as_float(b << 16); }
