@@ -1,0 +1,85 @@
+"""Products captured into a HIP graph, as the engine captures its decode step (src/cuda/core.rs:1151-1192): the
+launches allocate nothing and clear nothing with memsets, and the argmax table and the stream-K item counters return
+to zero inside the kernels, so every replay must give the eager results. The graph is replayed several times with new
+activations and eager launches between replays; each replay is checked against an eager run on the same inputs."""
+
+import numpy as np
+import pytest
+
+import oracle
+from qwenny_amd import Epi, Mat
+from qwenny_amd.synth import activations
+from tests.helpers import make_quant, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(gemm):
+    import torch
+
+    print("graph replays", flush=True)
+    k = 4096
+    dec = Mat.stack(gemm, [make_quant(91, "i4", 2048, k)])       # skinny, split-K partials
+    head = Mat.stack(gemm, [make_quant(92, "i4z", 8192, k)])     # skinny, argmax across workgroups
+    pre = Mat.stack(gemm, [make_quant(93, "i4", 4096, k)])       # prefill at 256 tokens: items spread (stream-K)
+    m_dec, m_pre = 1, 256
+    x_dec = torch.empty((m_dec, k), dtype=torch.bfloat16, device="cuda")
+    x_pre = torch.empty((m_pre, k), dtype=torch.bfloat16, device="cuda")
+    split = dec.split(m_dec)
+    y_dec = torch.empty((split, m_dec, dec.rows), dtype=torch.float32, device="cuda")
+    y_head = torch.empty((m_dec, head.rows), dtype=torch.float32, device="cuda")
+    keys = torch.zeros(m_dec, dtype=torch.int64, device="cuda")
+    y_pre = torch.empty((1, m_pre, pre.rows), dtype=torch.float32, device="cuda")
+
+    def step(stream):
+        gemm.run(stream, m_dec, dec, x_dec, y_dec, Epi.Plain)
+        gemm.run(stream, m_dec, head, x_dec, y_head, Epi.Argmax, n_out=m_dec, keys=keys)
+        gemm.run(stream, m_pre, pre, x_pre, y_pre, Epi.Plain)
+
+    def outputs():
+        return y_dec.sum(0).cpu().numpy(), y_head.cpu().numpy(), keys.cpu().numpy().view(np.uint64).copy(), \
+            y_pre.cpu().numpy()
+
+    def load_inputs(seed):
+        x_dec.copy_(to_dev(activations(seed, "x", m_dec, k)))
+        x_pre.copy_(to_dev(activations(seed + 1, "x", m_pre, k)))
+        keys.zero_()  # the caller clears keys before a step (embed does in the reference), a fill kernel here
+
+    load_inputs(1)
+    step(None)  # first launches outside the capture
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        load_inputs(10 + 2 * rep)
+        torch.cuda.synchronize()
+        step(None)  # eager
+        torch.cuda.synchronize()
+        want = outputs()
+        keys.zero_()
+        y_dec.fill_(float("nan"))
+        y_head.fill_(float("nan"))
+        y_pre.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = outputs()
+        for a, b in zip(got, want):
+            assert np.array_equal(a, b), rep
+        assert (got[2] == oracle.argmax_keys(got[1], head.rows)).all(), rep
+
+
+def test_empty_step_launches_nothing(gemm):
+    """n = 0 tokens: the product returns split 1 and touches nothing (the reference's empty-step path)."""
+    import torch
+
+    mat = Mat.stack(gemm, [make_quant(94, "i4", 256, 512)])
+    x = torch.zeros((1, 512), dtype=torch.bfloat16, device="cuda")
+    y = torch.full((1, 256), 7.0, dtype=torch.float32, device="cuda")
+    assert gemm.run(None, 0, mat, x, y, Epi.Plain) == 1
+    torch.cuda.synchronize()
+    assert (y.cpu().numpy() == 7.0).all()
