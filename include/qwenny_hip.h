@@ -131,7 +131,9 @@ int qh_unpack_row_bf16(size_t rows, size_t cols, const void* codes, size_t p, ui
 
 /* ---- device: context, matrices, products ---------------------------------------------------------------------- */
 
-/* Gemm::load (core.rs:436-481): a context on `device` (makes it current on this thread). */
+/* Gemm::load (core.rs:436-481): a context on `device` (makes it current on this thread). It holds the argmax scratch
+ * table and the prefill's stream-K scratch (128 MiB of partial tiles and 4096 item counters), both returned to zero by
+ * every launch; products on one context must therefore not run concurrently on two streams. */
 int qh_open(int device, qh_ctx** out);
 void qh_close(qh_ctx* ctx);
 
