@@ -458,6 +458,21 @@ def main():
         ms8 = time_step(st, args.steps, args.warmup, not args.no_graph)
         extra["int8_m1_GBps"] = round(st.bytes() / (ms8 * 1e-3) / 1e9, 1)
         print(f"# int8 M=1: {ms8:.4f} ms/step, {extra['int8_m1_GBps']} GB/s", file=sys.stderr, flush=True)
+        st5 = Step(gemm, 5, 17408)  # configs[4] at M = 5 and 2048 as well
+        for c in range(4):
+            for mats, (k, n) in zip(i8, [(5120, 17408), (17408, 5120)]):
+                st5.add(mats[c], Epi.Plain, int8_bytes(k, n, 5), 2 * 5 * k * n)
+        ms85 = time_step(st5, args.steps, args.warmup, not args.no_graph)
+        extra["int8_m5_GBps"] = round(st5.bytes() / (ms85 * 1e-3) / 1e9, 1)
+        pf8 = {}
+        for mats, (k, n) in zip(i8, [(5120, 17408), (17408, 5120)]):
+            stp = Step(gemm, 2048, k)
+            stp.add(mats[0], Epi.Plain, int8_bytes(k, n, 2048), 2 * 2048 * k * n)
+            msp = time_step(stp, max(10, args.steps // 10), 3, False)
+            pf8[f"{k}x{n}"] = round(stp.flops() / (msp * 1e-3) / 1e12, 1)
+        extra["int8_prefill_m2048_TFLOPs"] = pf8
+        print(f"# int8 M=5: {ms85:.4f} ms/step, {extra['int8_m5_GBps']} GB/s; M=2048: {pf8} TFLOP/s",
+              file=sys.stderr, flush=True)
     if "dense" in only:
         extra.update(dense_lines(gemm, args))
     if "dequant" in only:
