@@ -97,6 +97,10 @@ int qh_quant_zero_points(const qh_quant* q, uint8_t* z);
 /* Quant::row_into (checkpoint.rs:39-47): row r dequantized into out[cols] (f32). */
 int qh_quant_row_into(const qh_quant* q, size_t r, float* out);
 
+/* Quant::to_bf16 (checkpoint.rs:50-68): all rows dequantized (row_into) and rounded to bf16 nearest even into
+ * out[rows * cols], threaded over rows. */
+int qh_quant_to_bf16(const qh_quant* q, uint16_t* out);
+
 /* row_order (core.rs:108-114): packed row i <- original row out[i]. silu: gate/up interleaved per 16 rows. */
 int qh_row_order(size_t rows, int silu, size_t* out);
 

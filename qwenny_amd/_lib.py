@@ -42,6 +42,7 @@ SIGNATURES = {
     "qh_mat_quant_rows": (I, [P, ctypes.POINTER(QuantC), P, P, S, S, ctypes.POINTER(P)]),
     "qh_mat_dense_int8": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
     "qh_mat_dense": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
+    "qh_quant_to_bf16": (I, [ctypes.POINTER(QuantC), P]),
     "qh_dequant": (I, [P, P, P, P, S, S, S, I, I, S, S, P, I]),
     "qh_sum_parts": (I, [P, P, I, S, S, P]),
     "qh_add_rmsnorm": (I, [P, P, P, I, S, S, P, P, ctypes.c_float]),

@@ -103,10 +103,10 @@ class Quant:
         return out
 
     def to_bf16(self):
-        """All rows dequantized, as bf16 bits rounded to nearest even (src/checkpoint.rs:50-68)."""
-        from .synth import f32_to_bf16
-
-        return np.stack([f32_to_bf16(self.row_into(r)) for r in range(self.rows)])
+        """All rows dequantized, as bf16 bits rounded to nearest even (src/checkpoint.rs:50-68), threaded over rows."""
+        out = np.empty((self.rows, self.cols), np.uint16)
+        check(lib().qh_quant_to_bf16(ctypes.byref(self.c()), _np_ptr(out)))
+        return out
 
     def zero_points(self):
         """The integer zero point of each group if every offset is -z * scale (src/checkpoint.rs:72-82), else None."""

@@ -135,6 +135,20 @@ extern "C" int qh_quant_row_into(const qh_quant* q, size_t r, float* out) {
     return QH_OK;
 }
 
+// Quant::to_bf16 (checkpoint.rs:50-68): every row through row_into, rounded to bf16 nearest even, threaded over rows
+extern "C" int qh_quant_to_bf16(const qh_quant* q, uint16_t* out) {
+    if (int e = check_quant(q)) return e;
+    if (!out) return fail(QH_EINVAL, "to_bf16: null output");
+    parallel(q->rows, [&](size_t lo, size_t hi) {
+        std::vector<float> row(q->cols);
+        for (size_t r = lo; r < hi; r++) {
+            qh_quant_row_into(q, r, row.data());
+            for (size_t c = 0; c < q->cols; c++) out[r * q->cols + c] = f32_to_bf16(row[c]);
+        }
+    });
+    return QH_OK;
+}
+
 // row_order (cuda/core.rs:108-114)
 extern "C" int qh_row_order(size_t rows, int silu, size_t* out) {
     if (!out) return fail(QH_EINVAL, "row order: null output");

@@ -145,12 +145,14 @@ def test_row_order_matches_oracle():
             assert np.array_equal(row_order(rows, silu), oracle.row_order(rows, silu))
 
 
-def test_to_bf16():
-    q = make_quant(2, "i4z", 16, 256)
-    b = q.to_bf16()
+@pytest.mark.parametrize("kind,rows", [("i4z", 16), ("i4", 97 * 16), ("i8", 40)])
+def test_to_bf16(kind, rows):
+    """Quant::to_bf16 (threaded over rows) against torch's nearest-even rounding of each row_into row."""
     import torch
 
-    want = torch.from_numpy(np.stack([q.row_into(r) for r in range(16)])).to(torch.bfloat16).view(torch.int16)
+    q = make_quant(2, kind, rows, 256)
+    b = q.to_bf16()
+    want = torch.from_numpy(np.stack([q.row_into(r) for r in range(rows)])).to(torch.bfloat16).view(torch.int16)
     assert np.array_equal(b.view(np.int16), want.numpy())
 
 
