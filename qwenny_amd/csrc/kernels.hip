@@ -554,6 +554,10 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // while step s16's MFMAs run
     auto compute = [&](int buf, int hh, const WFrag& w) {
         const uint8_t* lb = lds + buf * STAGE;
+        // raised issue priority while this wave's MFMAs run: of the SIMD's waves, the one in its MFMA phase issues
+        // first and the other fills the gaps with its loads, LDS stores and barrier (measured: equal or faster on
+        // every prefill shape, +9% on (17408, 5120) at 512 tokens)
+        __builtin_amdgcn_s_setprio(1);
         u32x4 xa[2][BMB];
 #pragma unroll
         for (int bb = 0; bb < BMB; bb++) xa[0][bb] = *(const u32x4*)(lb + xr[0] + bb * 32 * PF_ROW);
@@ -572,6 +576,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
 #pragma unroll
                 for (int t = 0; t < TN; t++) acc[bb][t] = mfma32(xa[s16 & 1][bb], bw[t], acc[bb][t]);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // acc = the current item's product over groups [g0, g1): stage s is computed from one LDS buffer while stage
