@@ -162,3 +162,22 @@ def test_stack():
     assert s.rows == 48 and np.array_equal(s.q[16:], b.q) and np.array_equal(s.scales[:32], a.scales)
     with pytest.raises(ValueError):
         Quant.stack([a, make_quant(3, "i4", 16, 384)])
+
+
+def test_dense_bf16_rejects():
+    """Shape guards of the dense storage (rows of 16, columns of 128), and the int4/int8 unpacker refusing it."""
+    from qwenny_amd._lib import QhError
+
+    w = np.zeros((16, 100), np.uint16)
+    with pytest.raises(QhError):
+        packed_sizes(Wt.BF16, 16, 100)
+    with pytest.raises(QhError):
+        pack_dense_bf16(w, np.arange(16))
+    with pytest.raises(QhError):
+        pack_dense_bf16(np.zeros((24, 128), np.uint16), np.arange(24))  # 24 rows: not whole tiles
+    codes = pack_dense_bf16(np.zeros((16, 128), np.uint16), np.arange(16))
+    with pytest.raises(QhError):
+        unpack_rows(Wt.BF16, 16, 128, codes, np.zeros(0, np.uint8))
+    q = make_quant(5, "i4", 16, 128)
+    with pytest.raises(QhError):
+        pack_quant(q, np.arange(16), Wt.BF16)
