@@ -13,9 +13,9 @@
 // the grid (the split-K partials of the output contract).
 //
 // prefill_kernel (m > 16): MFMA-bound. A workgroup of 8 waves computes up to 256 tokens x 256 outputs; the
-// activation tile goes through double-buffered, XOR-swizzled LDS in 64-column stages, each wave dequantizes its own
-// outputs' weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), and the
-// workgroups are mapped XCD-aware so that those sharing a weight tile run on one XCD's L2.
+// activation tile goes global -> LDS directly (global_load_lds) into double-buffered, XOR-swizzled 64-column stages,
+// each wave dequantizes its own outputs' weights straight from global memory into bf16 registers ((q - z) s in f32,
+// rounded once), and the workgroups are mapped XCD-aware so that those sharing a weight tile run on one XCD's L2.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -237,8 +237,8 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
 #pragma unroll
         for (int t = 0; t < T && !(F & F_BF16); t++) {
             const size_t si = scale_idx(tt[t], G, gw, l16);
-            if (NG == 4) {
-                if (F & F_S32) {
+            if constexpr (NG == 4) {
+                if constexpr ((F & F_S32) != 0) {
                     const u32x4 v = *(const u32x4*)((const float*)a.scales + si);
                     sraw[t][0] = v.x, sraw[t][1] = v.y, sraw[t][2] = v.z, sraw[t][3] = v.w;
                 } else {
@@ -387,9 +387,9 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
 // hold its output row's columns for k16 steps 2i (first piece, word i) and 2i + 1 (second piece, word i).
 //
 // A workgroup of WM x WN waves computes WM * BMB * 32 tokens x WN * TN * 32 outputs; wave (wm, wn) owns BMB token
-// blocks x TN output blocks (BMB * TN accumulators of 16 registers). Activations go through double-buffered,
-// XOR-swizzled LDS in stages of 64 columns; each wave dequantizes its outputs' weights straight from global memory into
-// bf16 registers ((q - z) s in f32, rounded once).
+// blocks x TN output blocks (BMB * TN accumulators of 16 registers). Activations go global -> LDS directly
+// (global_load_lds_dwordx4, no register round trip) into double-buffered, XOR-swizzled stages of 64 columns; each wave
+// dequantizes its outputs' weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once).
 //
 // Work distribution. A work item is one workgroup tile. Whole items go to the first dp_items workgroups, ordered
 // XCD-aware (token tiles fastest, so that workgroups sharing a weight tile share an XCD's L2). When whole items would
@@ -408,22 +408,16 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
 }
 
-#ifndef QH_PF_BK
-#define QH_PF_BK 64
-#endif
-
-constexpr int PF_BK = QH_PF_BK;      // columns per LDS stage (64: half a group, or 128)
+constexpr int PF_BK = 64;            // columns per LDS stage (half a group; 128-column stages measured the same)
 constexpr int PF_ROW = PF_BK * 2;    // LDS bytes per token row of a stage
-constexpr int PF_KC = PF_BK / 8;     // 16-byte chunks per row of a stage
-constexpr int PF_SPG = QG / PF_BK;   // stages per group
 constexpr int PF_K16 = PF_BK / 16;   // k16 steps per stage
-static_assert(PF_SPG * PF_BK == QG && (PF_KC == 8 || PF_KC == 16), "a stage is half a group or one group");
 
-// LDS byte offset of 16-byte chunk kc of token row `row` in a stage: XOR-swizzled so that 16 lanes reading 16
-// consecutive rows at one chunk hit all 64 banks once (rows of 128 bytes pair up in one 256-byte bank line).
-__device__ __forceinline__ int pf_lds_off(int row, int kc) {
-    return row * PF_ROW + 16 * (PF_KC == 8 ? kc ^ ((row >> 1) & 7) : kc ^ (row & 15));
-}
+// LDS byte offset of 16-byte chunk kc (0..7) of token row `row` in a stage: XOR-swizzled so that 16 lanes reading
+// 16 consecutive rows at one chunk hit all 64 banks once (rows of 128 bytes pair up in one 256-byte bank line).
+__device__ __forceinline__ int pf_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW + 16 * (kc ^ pf_swz(row)); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // Stream-K ranges: U units over P workgroups, q = U / P (at least 1) each and one more for the first r = U % P.
 // The first unit of workgroup s, and the workgroup whose range holds unit u:
@@ -434,19 +428,21 @@ __device__ __forceinline__ int sk_owner(int u, int q, int r) {
 
 template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB>
 __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
-    constexpr int NTHR = WM * WN * 64;
     constexpr int BM = WM * BMB * 32;                // tokens per workgroup
     constexpr int WTILES = WN * TN * 2;              // 16-row tiles per workgroup
-    constexpr int CPT = BM * (PF_ROW / 16) / NTHR;   // 16-byte x pieces each thread stages per stage
-    static_assert(CPT >= 1 && CPT * NTHR == BM * (PF_ROW / 16), "stage pieces must divide over the threads");
     constexpr int CW = CodeWords<F>::N;
     constexpr int STAGE = BM * PF_ROW;               // LDS bytes of one stage
     constexpr int NW = WM * WN;                      // waves
     constexpr int NACC = BMB * TN * 16;              // accumulator registers per lane
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+    // two objects, so that the compiler can tell the direct-to-LDS loads into one from the reads of the other
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
+    constexpr int NI = STAGE / 1024 / NW;  // 1 KiB direct-to-LDS loads per wave per stage
+    static_assert(NI >= 1 && NI * 1024 * NW == STAGE, "stage blocks must divide over the waves");
+    uint32_t xd[NI];                       // per-lane global byte offsets of those loads (stage 0)
     __shared__ int sk_last;
 
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), tid = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave % WM, wn = wave / WM;
     const int l32 = lane & 31, lh = lane >> 5, l16 = lane & 15;
     const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
@@ -455,25 +451,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     const int wtok0 = wm * BMB * 32;  // the wave's first token row in the stage
     int tok0 = 0, tile0 = 0;          // the current item's first token and the wave's first tile
 
-    // Global loads take a wave-uniform base plus a 32-bit per-lane byte offset fixed for the whole kernel (no 64-bit
-    // address arithmetic per load). Activations: piece c = tid + NTHR i -> row c / 8, column chunk c % 8.
+    // Global loads take a wave-uniform base plus a 32-bit per-lane byte offset fixed for the item (no 64-bit address
+    // arithmetic per load).
     const uint8_t* xbase = (const uint8_t*)a.x;
-    uint32_t xg[CPT];
-    int xs[CPT];
-#pragma unroll
-    for (int i = 0; i < CPT; i++) {
-        const int c = tid + NTHR * i;
-        xs[i] = pf_lds_off(c / PF_KC, c % PF_KC);
-    }
-    auto stage_load = [&](int s, u32x4 (&v)[CPT]) {
-        const uint8_t* p = xbase + (size_t)s * PF_ROW;
-#pragma unroll
-        for (int i = 0; i < CPT; i++) v[i] = *(const u32x4*)(p + xg[i]);
-    };
-    auto stage_store = [&](int buf, const u32x4 (&v)[CPT]) {
-#pragma unroll
-        for (int i = 0; i < CPT; i++) *(u32x4*)(lds + buf * STAGE + xs[i]) = v[i];
-    };
     // LDS reads of A fragments: row wtok0 + 32 bb + l32, chunk 2 s16 + lh; the swizzle of rows 32 bb + l32 depends on
     // l32 only, so the per-lane part is 4 offsets and the token block is an immediate
     int xr[PF_K16];
@@ -487,11 +467,14 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     auto set_item = [&](int item) {
         tok0 = (item % ntok) * BM;
         tile0 = (item / ntok) * WTILES + wn * TN * 2;
+        // activations: load i of this wave fills LDS block i NW + wave, whose lane l writes row 8 block + l / 8, slot
+        // l % 8; that slot holds column chunk slot ^ swizzle(row), so the lane fetches that chunk (rows past M read
+        // row M - 1: their results are never stored)
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + NTHR * i, row = c / PF_KC, kc = c % PF_KC;
+        for (int i = 0; i < NI; i++) {
+            const int row = 8 * (i * NW + wave) + (lane >> 3), kc = (lane & 7) ^ pf_swz(row);
             const int tok = min(tok0 + row, M - 1);
-            xg[i] = (uint32_t)(((size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc) * 2);
+            xd[i] = (uint32_t)(((size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * kc) * 2);
         }
 #pragma unroll
         for (int t = 0; t < TN; t++) {
@@ -553,7 +536,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // one stage (64 columns, half hh of the group) from LDS buffer `buf`: the A fragments of k16 step s16 + 1 are read
     // while step s16's MFMAs run
     auto compute = [&](int buf, int hh, const WFrag& w) {
-        const uint8_t* lb = lds + buf * STAGE;
+        const uint8_t* lb = buf ? lds1 : lds0;
         // raised issue priority while this wave's MFMAs run: of the SIMD's waves, the one in its MFMA phase issues
         // first and the other fills the gaps with its loads, LDS stores and barrier (measured: equal or faster on
         // every prefill shape, +9% on (17408, 5120) at 512 tokens)
@@ -579,35 +562,43 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         __builtin_amdgcn_s_setprio(0);
     };
 
-    // acc = the current item's product over groups [g0, g1): stage s is computed from one LDS buffer while stage
-    // s + 1 is loaded into registers and then stored to the other buffer; the next group's weights are loaded one
-    // group ahead.
+    // acc = the current item's product over groups [g0, g1). The activations go global -> LDS directly
+    // (global_load_lds_dwordx4): stage 2g (the group's first 64 columns) is computed from lds0 while stage 2g + 1 loads
+    // into lds1 and the next group's weights into registers, then stage 2g + 1 from lds1 while stage 2g + 2 loads into
+    // lds0; each stage ends with a wait for its activation loads (the weight loads issued after them may stay in
+    // flight) and one barrier.
+    auto stage_issue = [&](int st, uint8_t* buf) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            __builtin_amdgcn_global_load_lds((const void*)(xbase + (size_t)st * PF_ROW + xd[i]),
+                                             (lds_ptr)(buf + (i * NW + wave) * 1024), 16, 0, 0);
+    };
+    // weight loads a wload issues (code pieces, scale, zero point): what may stay in flight after a stage's x loads
+    constexpr int WLOADS = TN * (2 * CW + ((F & (F_PERCH | F_BF16)) ? 0 : 1) + ((F & F_ZP) ? 1 : 0));
     auto run = [&](int g0, int g1) {
         clear();
-        u32x4 xv[CPT];
         WFrag wcur, wnxt;
-        const int s1 = g1 * PF_SPG;  // stages of [g0, g1): stage s holds columns s * PF_BK ..
-        int buf = 0;
-        stage_load(g0 * PF_SPG, xv);
+        stage_issue(2 * g0, lds0);
         wload(g0, wcur);
-        stage_store(0, xv);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         for (int g = g0; g < g1; g++) {
-#pragma unroll
-            for (int hh = 0; hh < PF_SPG; hh++) {
-                const int s = g * PF_SPG + hh;
-                const bool more = s + 1 < s1;
-                if (more) stage_load(s + 1, xv);
-                if (hh == 0) wload(g + 1 < g1 ? g + 1 : g, wnxt);
-                compute(buf, hh, wcur);
-                if (more) stage_store(buf ^ 1, xv);
-                __syncthreads();
-                buf ^= 1;
-            }
+            const bool more = g + 1 < g1;
+            // stage 2g from lds0 while stage 2g + 1 loads into lds1 (the next group's weights behind it)
+            stage_issue(2 * g + 1, lds1);
+            __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the x loads (the wait below counts on it)
+            wload(more ? g + 1 : g, wnxt);
+            compute(0, 0, wcur);
+            // x loads done, the weight loads issued after them may stay in flight
+            __builtin_amdgcn_s_waitcnt((WLOADS & 15) | ((WLOADS >> 4) << 14) | (7 << 4) | (15 << 8));
+            __syncthreads();
+            if (more) stage_issue(2 * g + 2, lds0);
+            compute(1, 1, wcur);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
             wcur = wnxt;
         }
     };
-
     // epilogue of the current item: acc[bb][t][v] = D[token tok0 + wtok0 + 32 bb + 8 (v / 4) + 4 lh + v % 4]
     // [output 32-block t, l32]
     auto epilogue = [&]() {
