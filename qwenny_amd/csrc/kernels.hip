@@ -626,7 +626,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
                         if (tile_ok && l16 < 8 && tok < M)
                             ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(val) * up);
                     } else {
-                        if (tile_ok && tok < M) ((float*)a.y)[(size_t)tok * a.ldy + out] = val;
+                        // streamed past the caches: the outputs are not read again here, the tiles still are
+                        if (tile_ok && tok < M) __builtin_nontemporal_store(val, (float*)a.y + (size_t)tok * a.ldy + out);
                         if (EPI == EPI_ARGMAX && tile_ok && tok < M && out < a.valid)
                             key[bb][v] = max_u64(key[bb][v], argmax_key(val, out));
                     }
