@@ -104,7 +104,8 @@ int qh_quant_to_bf16(const qh_quant* q, uint16_t* out);
 /* row_order (core.rs:108-114): packed row i <- original row out[i]. silu: gate/up interleaved per 16 rows. */
 int qh_row_order(size_t rows, int silu, size_t* out);
 
-/* Byte sizes of the gfx950 tile layout for a matrix of `rows` packed rows (padded up to 16) and `cols` columns. */
+/* Byte sizes of the gfx950 tile layout for a matrix of `rows` packed rows (a multiple of 16) and `cols` columns (of 128).
+ * The codes of one matrix must fit in 4 GiB (the kernels use 32-bit offsets): QH_EINVAL beyond. */
 int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_bytes, size_t* scale_bytes, size_t* zero_bytes);
 
 /* The load-time repacker: rows `order[0..n)` of `q` (a Quant of bits 4 or 8, group a multiple of 128 or a whole row)
@@ -181,6 +182,7 @@ size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, s
  *   epi QH_EPI_ARGMAX: logit rows: token t reads x row out_rows[t] (int32 device, NULL: t) for t < n_out; y f32
  *     [n_out][rows]; keys[t] (u64 device, cleared by the caller) = max(keys[t], (ordered(v) << 32) | ~o) over the
  *     valid rows o.
+ * Above 16 tokens x's rows 0 .. max(n, n_out) - 1 must lie within 4 GiB of x (32-bit offsets): QH_EINVAL beyond.
  * Returns the split (>= 1) or < 0. Launches only: no host synchronisation, no allocation (graph-capturable). */
 int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, const int32_t* out_rows,
             size_t n_out, void* y, int epi, uint64_t* keys, int whole);

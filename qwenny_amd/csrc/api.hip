@@ -323,6 +323,10 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     if (epi == QH_EPI_ARGMAX && m > (size_t)ARGMAX_MAX_TOK)
         return fail(QH_EINVAL, "argmax over %zu logit rows: at most %d", m, ARGMAX_MAX_TOK);
     if (m > (1u << 24) || w->rows > (1u << 30) || ldx > (1u << 30)) return fail(QH_EINVAL, "gemm: sizes too large");
+    // the prefill kernel addresses activation rows (the n token rows, also those the argmax gathers) with 32-bit byte
+    // offsets from x
+    if (m > (size_t)SKINNY_MAX_M && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
+        return fail(QH_EINVAL, "gemm: %zu token rows of %zu elements: x must fit in 4 GiB", n, ldx);
     Launch l{};
     l.codes = w->codes;
     l.scales = w->scales;

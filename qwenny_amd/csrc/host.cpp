@@ -164,6 +164,9 @@ extern "C" int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_by
     if (rows == 0 || rows % TILE || cols == 0 || cols % QG)
         return fail(QH_EINVAL, "%zu x %zu: rows must be a multiple of 16, columns of 128", rows, cols);
     size_t tiles = rows / TILE, blocks = tiles * (cols / QG), qd = tiles * quads(cols / QG);
+    // the kernels address codes and scales with 32-bit byte offsets from the matrix's base
+    if (rows > (1u << 30) || cols > (1u << 30) || blocks * block_bytes(wt) > 0xffffffffu)
+        return fail(QH_EINVAL, "%zu x %zu: the codes must fit in 4 GiB", rows, cols);
     if (code_bytes) *code_bytes = blocks * block_bytes(wt);
     if (scale_bytes) *scale_bytes = has_scales(wt) ? qd * TILE * 4 * (f32_scales(wt) ? 4 : 2) : 0;
     if (zero_bytes) *zero_bytes = has_zeros(wt) ? qd * TILE * 2 : 0;

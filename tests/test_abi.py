@@ -48,6 +48,10 @@ def test_errors_report():
     assert "multiple of 16" in lib().qh_last_error().decode()
     with pytest.raises(QhError):
         packed_sizes(7, 16, 128)
+    with pytest.raises(QhError) as e:  # codes past 32-bit offsets: 2^31 16-bit weights
+        packed_sizes(Wt.BF16, 1 << 17, 1 << 14)
+    assert "4 GiB" in str(e.value)
+    assert packed_sizes(Wt.I4, 248320, 5120)[0] == 248320 * 5120 // 2
     q = make_quant(1, "i4", 32, 256)
     with pytest.raises(QhError):  # 8-bit storage for a 4-bit matrix
         pack_quant(q, np.arange(32), Wt.I8)

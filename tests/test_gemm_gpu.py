@@ -158,3 +158,18 @@ def test_argmax_rejects_too_many_rows(gemm):
     keys = torch.zeros(65, dtype=torch.int64, device="cuda")
     with pytest.raises(QhError):
         gemm.run(None, 65, mat, x, y, Epi.Argmax, n_out=65, keys=keys)
+
+
+def test_prefill_rejects_x_past_32bit_offsets(gemm):
+    """Above 16 tokens the kernels address x's rows with 32-bit byte offsets: a row stride that puts token 16 at 4 GiB
+    is refused before any launch."""
+    import torch
+
+    from qwenny_amd._lib import QhError
+
+    mat = Mat.stack(gemm, [make_quant(45, "i4", 64, 128)])
+    x = torch.zeros((17, 128), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((17, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(QhError) as e:
+        gemm.run(None, 17, mat, x, y, Epi.Plain, ldx=1 << 27)
+    assert "4 GiB" in str(e.value)
