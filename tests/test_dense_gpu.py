@@ -48,6 +48,19 @@ def test_dense_plain(gemm, m):
     assert rel_err(got, oracle.dense_f64(w, x, f16_weights=True)) <= TOL
 
 
+@pytest.mark.parametrize("m", [1, 5, 300])
+def test_dense_in_ba_shape(gemm, m):
+    """The 27B DeltaNet in_ba projection (K 5120, N 96), which stays 16-bit in a pre-quantized checkpoint: 6 tiles,
+    fewer than any wave column or prefill workgroup covers."""
+    print(f"dense in_ba m={m}", flush=True)
+    rows, cols = 96, 5120
+    w = _weights(71 + m, rows, cols)
+    x = activations(72 + m, "x", m, cols)
+    mat = Mat.new(gemm, w, cols, int8=False)
+    got = _plain(gemm, mat, x, m)
+    assert rel_err(got, oracle.dense_f64(w, x)) <= 1e-4
+
+
 @pytest.mark.parametrize("m", [1, 40])
 def test_dense_silu(gemm, m):
     import torch
