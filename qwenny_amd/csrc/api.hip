@@ -25,7 +25,7 @@ struct qh_ctx {
     int skinny_tile_waves;  // skinny kernel, plain products: waves side by side over tiles (0: by token count)
     int pf_shape;           // prefill workgroup shape (0: by tail waste; QH_PF_SHAPE for tuning sweeps)
     // prefill stream-K: partial tiles, then PF_SK_ITEMS_MAX item counters (zeroed here, left zero by every launch);
-    // QH_PF_SK=0 turns it off (tuning)
+    // QH_PF_SK=0 turns it off, a value above 1 replaces the launcher's fix-up cost (tuning)
     void* sk_scratch;
     int stream_k;
 };
@@ -85,7 +85,7 @@ extern "C" int qh_open(int device, qh_ctx** out) {
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
                       std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
-                      std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, env_int("QH_PF_SK", 1) != 0};
+                      std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1))};
     return QH_OK;
 }
 

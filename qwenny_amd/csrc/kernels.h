@@ -40,7 +40,7 @@ struct Launch {
     int cus;                // compute units (the prefill shape choice)
     int pf_shape;           // prefill workgroup shape: 0 chosen by size, else forced (kernels.hip prefill_epi)
     // prefill stream-K (kernels.hip prefill_kernel): scratch of partial tiles (PF_SK_PART_BYTES) and PF_SK_ITEMS_MAX
-    // item counters (zero between launches); stream_k = 0 turns it off. Set by the launcher: dp_items, sk_items,
+    // item counters (zero between launches); stream_k = 0 turns it off, above 1 it is the fix-up cost (tuning). Set by the launcher: dp_items, sk_items,
     // sk_wgs and the stream-K ranges (sk_q units per workgroup, one more for the first sk_r).
     float* sk_part;
     unsigned* sk_count;

@@ -419,6 +419,10 @@ __device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// buffer resource word 3 (gfx9: 32-bit data format, no swizzle) and the sc1 cache-policy bit of buffer operations
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
+constexpr int CPOL_SC1 = 16;
+
 // Stream-K ranges: U units over P workgroups, q = U / P (at least 1) each and one more for the first r = U % P.
 // The first unit of workgroup s, and the workgroup whose range holds unit u:
 __device__ __forceinline__ int sk_begin(int s, int q, int r) { return s * q + min(s, r); }
@@ -664,6 +668,14 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         u = dp * G + sk_begin(s, a.sk_q, a.sk_r);
         u1 = dp * G + sk_begin(s + 1, a.sk_q, a.sk_r);
     }
+    // the stream-K partials, as a buffer resource: 16-byte loads and stores with the agent-coherence cache policy
+    // (sc1, what agent-scope atomics use), at byte offsets [slot][wave][register / 4][lane][4] f32
+    constexpr int NQ = NACC / 4, SK_QC = NQ >= 32 ? 16 : NQ / 2;
+    const __amdgpu_buffer_rsrc_t skr = __builtin_amdgcn_make_buffer_rsrc(a.sk_part, 0, (int)PF_SK_PART_BYTES,
+                                                                         BUF_RSRC_WORD3);
+    auto sk_off = [&](int slot, int w, int l) -> uint32_t {
+        return (uint32_t)((((size_t)slot * NW + w) * NQ * 64 + l) * 16);
+    };
     const int first_item = u / G;
     while (u < u1) {
         const int it = u / G, g0 = u - it * G, g1 = min(G, g0 + (u1 - u));
@@ -672,16 +684,15 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         u += g1 - g0;
         if (g0 != 0 || g1 != G) {
             // a cut item (stream-K): write this segment's partial to slot 2 s (+1 unless it is this workgroup's
-            // first item), as [wave][register][lane] f32, with device-coherent stores
-            float* part = a.sk_part + ((size_t)(2 * s + (it != first_item)) * NW + wave) * NACC * 64 + lane;
+            // first item), as [wave][register / 4][lane][4] f32, with 16-byte device-coherent stores
+            const uint32_t part = sk_off(2 * s + (it != first_item), wave, lane);
 #pragma unroll
-            for (int bb = 0; bb < BMB; bb++)
-#pragma unroll
-                for (int t = 0; t < TN; t++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++)
-                        __hip_atomic_store(part + ((bb * TN + t) * 16 + e) * 64, acc[bb][t][e], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+            for (int q = 0; q < NQ; q++) {
+                const f32x16& v = acc[(q >> 2) / TN][(q >> 2) % TN];
+                const int e = (q & 3) * 4;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]}),
+                                                       skr, part + q * 1024, 0, CPOL_SC1);
+            }
             __builtin_amdgcn_s_waitcnt(0);  // this wave's partial has been performed
             __syncthreads();
             const int sit = it - dp, su = sit * G;  // the item among the stream-K ones, its first unit
@@ -695,18 +706,22 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             // that the sum does not depend on the order of arrival), 16 registers at a time
             clear();
             for (int o = sa; o <= sb; o++) {
-                const int slot = 2 * o + (sk_begin(o, a.sk_q, a.sk_r) < su);
-                const float* src = a.sk_part + ((size_t)slot * NW + wave) * NACC * 64 + lane;
+                const uint32_t src = sk_off(2 * o + (sk_begin(o, a.sk_q, a.sk_r) < su), wave, lane);
 #pragma unroll
-                for (int bb = 0; bb < BMB; bb++)
+                for (int q0 = 0; q0 < NQ; q0 += SK_QC) {
+                    f32x4 v[SK_QC];
 #pragma unroll
-                    for (int t = 0; t < TN; t++) {
+                    for (int i = 0; i < SK_QC; i++)
+                        v[i] = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(skr, src + (q0 + i) * 1024, 0, CPOL_SC1));
 #pragma unroll
-                        for (int e = 0; e < 16; e++)
-                            acc[bb][t][e] += __hip_atomic_load(src + ((bb * TN + t) * 16 + e) * 64,
-                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __builtin_amdgcn_sched_barrier(0);
+                    for (int i = 0; i < SK_QC; i++) {
+                        const int q = q0 + i, e = (q & 3) * 4;
+                        f32x16& d = acc[(q >> 2) / TN][(q >> 2) % TN];
+                        d[e] += v[i][0], d[e + 1] += v[i][1], d[e + 2] += v[i][2], d[e + 3] += v[i][3];
                     }
+                    __builtin_amdgcn_sched_barrier(0);  // one chunk of loads in flight at a time (registers)
+                }
             }
             if (threadIdx.x == 0)
                 (void)__hip_atomic_exchange(a.sk_count + sit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -774,7 +789,8 @@ static hipError_t prefill_cfg(const Launch& l0) {
         const size_t slot = (size_t)bm * wg_tiles * TILE * 4;
         const long sk = rounds >= 2 ? items - (rounds - 2) * P : items;
         const long U = sk * G;
-        const long t_dp = rounds * G, t_sk = (rounds >= 2 ? (rounds - 2) * G : 0) + (U + P - 1) / P + PF_SK_FIXUP;
+        const long fixup = l.stream_k > 1 ? l.stream_k : PF_SK_FIXUP;
+        const long t_dp = rounds * G, t_sk = (rounds >= 2 ? (rounds - 2) * G : 0) + (U + P - 1) / P + fixup;
         if (t_sk * 20 < t_dp * 19 && 2 * P * slot <= PF_SK_PART_BYTES) {
             if (sk <= PF_SK_ITEMS_MAX && U >= P && items * G < (1l << 31)) {
                 l.dp_items = (int)(items - sk);
