@@ -85,7 +85,7 @@ extern "C" int qh_open(int device, qh_ctx** out) {
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
                       std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
-                      std::min(6, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1))};
+                      std::min(9, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1))};
     return QH_OK;
 }
 

@@ -442,8 +442,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // two objects, so that the compiler can tell the direct-to-LDS loads into one from the reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
-    constexpr int NI = STAGE / 1024 / NW;  // 1 KiB direct-to-LDS loads per wave per stage
-    static_assert(NI >= 1 && NI * 1024 * NW == STAGE, "stage blocks must divide over the waves");
+    constexpr int NB = STAGE / 1024;           // 1 KiB blocks of a stage
+    constexpr int NI = (NB + NW - 1) / NW;     // direct-to-LDS loads per wave per stage (block i NW + wave < NB)
+    static_assert(NB * 1024 == STAGE, "stages of whole 1 KiB blocks");
     uint32_t xd[NI];                       // per-lane global byte offsets of those loads (stage 0)
     __shared__ int sk_last;
 
@@ -575,6 +576,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     auto stage_issue = [&](int st, uint8_t* buf) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
+            if (NB % NW == 0 || i * NW + wave < NB)  // wave-uniform
             __builtin_amdgcn_global_load_lds((const void*)(xbase + (size_t)st * PF_ROW + xd[i]),
                                              (lds_ptr)(buf + (i * NW + wave) * 1024), 16, 0, 0);
     };
@@ -763,52 +765,62 @@ static hipError_t skinny_epi(const Launch& l) {
     }
 }
 
+// The launch plan of one prefill shape: whole items or stream-K for the tail, in l.dp_items / sk_*; returns the
+// estimated time in units of one group of K on one item of this shape.
+// Stream-K: the last P < sk_items <= 2 P items (all of them when there are at most 2 P) are spread over P = the
+// resident workgroups, when that is estimated faster: whole items take rounds * G; stream-K takes (rounds - 2) * G for
+// the whole rounds, ceil(U / P) for the spread units and PF_SK_FIXUP for the cut items (pipeline refills, writing and
+// summing partials; measured on MI355X: about 12 groups of K for 256 x 256 items, so a 75%-full single round of
+// K = 5120 stays whole).
 template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB = 1>
-static hipError_t prefill_cfg(const Launch& l0) {
-    Launch l = l0;
+static long prefill_plan(Launch& l) {
     const int tiles = l.rows / TILE, G = l.cols / QG;
     const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32, threads = WM * WN * 64;
     const long items = (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
-    auto kern = prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>;
-    // Stream-K: the last P < sk_items <= 2 P items (all of them when there are at most 2 P) are spread over P = the
-    // resident workgroups, when that is estimated faster in units of one group's compute: whole items take rounds * G;
-    // stream-K takes (rounds - 2) * G for the whole rounds, ceil(U / P) for the spread units and PF_SK_FIXUP for
-    // writing and summing the partials of cut items (measured on MI355X: a 256 x 256 partial costs about as much as
-    // 12 groups of K, so a 75%-full single round of K = 5120 stays whole).
     static int per_cu = -1;  // resident workgroups per CU (per instantiation; the same on every MI355X)
     if (per_cu < 0) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess) n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>, threads,
+                                                         0) != hipSuccess)
+            n = 0;
         per_cu = n;
     }
     const long P = (long)per_cu * l.cus;
     l.dp_items = (int)items;
     l.sk_items = 0;
     l.sk_wgs = 0;
-    if (l.stream_k && P > 0) {
-        const long rounds = (items + P - 1) / P;
-        const size_t slot = (size_t)bm * wg_tiles * TILE * 4;
-        const long sk = rounds >= 2 ? items - (rounds - 2) * P : items;
-        const long U = sk * G;
-        const long fixup = l.stream_k > 1 ? l.stream_k : PF_SK_FIXUP;
-        const long t_dp = rounds * G, t_sk = (rounds >= 2 ? (rounds - 2) * G : 0) + (U + P - 1) / P + fixup;
-        if (t_sk * 20 < t_dp * 19 && 2 * P * slot <= PF_SK_PART_BYTES) {
-            if (sk <= PF_SK_ITEMS_MAX && U >= P && items * G < (1l << 31)) {
-                l.dp_items = (int)(items - sk);
-                l.sk_items = (int)sk;
-                l.sk_wgs = (int)P;
-                l.sk_q = (int)(U / P);
-                l.sk_r = (int)(U % P);
-            }
-        }
+    if (P <= 0) return 1l << 40;
+    const long rounds = (items + P - 1) / P, t_dp = rounds * G;
+    if (!l.stream_k) return t_dp;
+    const size_t slot = (size_t)bm * wg_tiles * TILE * 4;
+    const long sk = rounds >= 2 ? items - (rounds - 2) * P : items;
+    const long U = sk * G;
+    const long fixup = l.stream_k > 1 ? l.stream_k : PF_SK_FIXUP;
+    const long t_sk = (rounds >= 2 ? (rounds - 2) * G : 0) + (U + P - 1) / P + fixup;
+    if (t_sk * 20 < t_dp * 19 && 2 * P * slot <= PF_SK_PART_BYTES && sk <= PF_SK_ITEMS_MAX && U >= P &&
+        items * G < (1l << 31)) {
+        l.dp_items = (int)(items - sk);
+        l.sk_items = (int)sk;
+        l.sk_wgs = (int)P;
+        l.sk_q = (int)(U / P);
+        l.sk_r = (int)(U % P);
+        return t_sk;
     }
-    hipLaunchKernelGGL(kern, dim3(l.dp_items + l.sk_wgs), dim3(threads), 0, l.stream, l);
+    return t_dp;
+}
+
+template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB = 1>
+static hipError_t prefill_cfg(const Launch& l0) {
+    Launch l = l0;
+    (void)prefill_plan<F, EPI, BMB, TN, WM, WN, MINB>(l);
+    hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>), dim3(l.dp_items + l.sk_wgs),
+                       dim3(WM * WN * 64), 0, l.stream, l);
     return hipGetLastError();
 }
 
 // The prefill workgroup shape (tokens x outputs; waves): the largest tile that still makes two waves per CU
-// (256 x 256 on 8 waves of 256 x 32, then 256 x 128 and 128 x 128 on 4 waves), 64 x 128 for the smallest steps;
-// QH_PF_SHAPE forces one in tuning sweeps.
+// (256 x 256 on 8 waves of 256 x 32, or 256 x 192 on 12 waves when that fills the CUs better; then 256 x 128 and
+// 128 x 128 on 4 waves), 64 x 128 for the smallest steps; QH_PF_SHAPE forces one in tuning sweeps.
 template <int F, int EPI>
 static hipError_t prefill_epi(const Launch& l) {
     const int tiles = l.rows / TILE;
@@ -817,8 +829,14 @@ static hipError_t prefill_epi(const Launch& l) {
     };
     int shape = l.pf_shape;
     if (shape == 0) {  // enough waves: at least two per CU
-        if (l.m > 128 && items(256, 16) * 8 >= 2 * l.cus) shape = 2;
-        else if (l.m > 128 && items(256, 8) * 4 >= 2 * l.cus) shape = 1;
+        if (l.m > 128 && items(256, 16) * 8 >= 2 * l.cus) {
+            shape = 2;
+            // 256 x 192 on 12 waves when its rounds fill the CUs enough better to outweigh its lower rate (items of
+            // 3/4 the work at about 0.85 of the rate of 256 x 256: (5120, 6144) at 2048 tokens fills all 256 CUs with
+            // it, 3/4 of them with 256 x 256, measured +10%)
+            Launch a = l, b = l;
+            if (prefill_plan<F, EPI, 4, 1, 2, 6>(a) * 15 < prefill_plan<F, EPI, 8, 1, 1, 8>(b) * 17) shape = 7;
+        } else if (l.m > 128 && items(256, 8) * 4 >= 2 * l.cus) shape = 1;
         else if (l.m > 64 && items(128, 8) * 4 >= 2 * l.cus) shape = 5;
         else shape = 6;
     }
@@ -828,6 +846,7 @@ static hipError_t prefill_epi(const Launch& l) {
         case 3: return prefill_cfg<F, EPI, 4, 2, 2, 4>(l);   // 256 x 256; 8 waves of 128 x 64
         case 4: return prefill_cfg<F, EPI, 8, 2, 1, 4>(l);   // 256 x 256; 4 waves of 256 x 64
         case 5: return prefill_cfg<F, EPI, 4, 1, 1, 4>(l);   // 128 x 128; 4 waves of 128 x 32
+        case 7: return prefill_cfg<F, EPI, 4, 1, 2, 6>(l);   // 256 x 192; 12 waves of 128 x 32
         default: return prefill_cfg<F, EPI, 2, 1, 1, 4>(l);  // 64 x 128; 4 waves of 64 x 32
     }
 }

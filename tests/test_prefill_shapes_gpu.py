@@ -1,0 +1,57 @@
+"""Parity of the 256 x 192 prefill workgroup shape (12 waves of 128 tokens x 32 outputs), which the launcher picks
+over 256 x 256 when its whole rounds fill the CUs better: whole items at (2048 tokens, K 2048, 6144 outputs) through
+the SwiGLU epilogue, and stream-K items at (512, 5120, 9216) through the plain one (a sample of rows). Same bars as the
+other prefill tests: the oracle to 2e-2 RMS, the kernel's own arithmetic (bf16-rounded weights) to 1e-4, and the
+SwiGLU output against silu over that arithmetic to 1e-3.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from qwenny_amd import Epi, Mat, row_order
+from qwenny_amd.synth import activations
+from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, sub_quant,
+                           to_dev)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
+def test_shape_256x192_stream_k_plain(gemm, kind):
+    import torch
+
+    print(f"prefill 256 x 192 stream-K plain {kind}", flush=True)
+    n, k, m = 9216, 5120, 512
+    q = make_quant(120, kind, n, k)
+    mat = Mat.stack(gemm, [q])
+    rows = np.sort(np.random.default_rng(6).choice(n, 384, replace=False))
+    sq = sub_quant(q, rows)
+    for rep in range(2):  # the item counters must be left at zero by each launch
+        x = activations(121 + rep, "x", m, k, outliers=0.01)
+        y = torch.full((1, m, n), float("nan"), dtype=torch.float32, device="cuda")
+        assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == 1
+        torch.cuda.synchronize()
+        got = y[0].cpu().numpy().astype(np.float64)
+        assert not np.isnan(got).any()
+        got = got[:, rows]
+        assert rel_err(got, oracle_y(sq, x)) <= TOL, rep
+        assert rel_err(got, emulate_bf16_weights(sq, x)) <= 1e-4, rep
+
+
+def test_shape_256x192_silu(gemm):
+    import torch
+
+    print("prefill 256 x 192 SwiGLU", flush=True)
+    n, k, m = 6144, 2048, 2048
+    gate = make_quant(130, "i4", n // 2, k)
+    up = make_quant(131, "i4", n // 2, k)
+    x = activations(132, "x", m, k, outliers=0.01)
+    mat = Mat.stack(gemm, [gate, up], silu=True)
+    y = torch.full((m, n // 2), float("nan"), dtype=torch.bfloat16, device="cuda")
+    assert gemm.run(None, m, mat, to_dev(x), y, Epi.Silu) == 1
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    full = np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
+    want = oracle.silu_glu(full, row_order(n, True))
+    assert bf16_out_err(got, want) <= 1e-3
