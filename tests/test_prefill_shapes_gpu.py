@@ -55,3 +55,23 @@ def test_shape_256x192_silu(gemm):
     full = np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
     want = oracle.silu_glu(full, row_order(n, True))
     assert bf16_out_err(got, want) <= 1e-3
+
+
+def test_shape_256x192_dense_bf16(gemm):
+    """Dense bf16 weights (the reference's Wt::F16) at the same stream-K shape: exact products, 1e-4 of RMS."""
+    import torch
+
+    from qwenny_amd.synth import f32_to_bf16
+
+    print("prefill 256 x 192 stream-K dense bf16", flush=True)
+    n, k, m = 9216, 5120, 512
+    w = f32_to_bf16(np.random.default_rng(140).standard_normal((n, k)).astype(np.float32) * 0.05)
+    mat = Mat.new(gemm, w, k, int8=False)
+    x = activations(141, "x", m, k, outliers=0.01)
+    y = torch.full((1, m, n), float("nan"), dtype=torch.float32, device="cuda")
+    assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == 1
+    torch.cuda.synchronize()
+    got = y[0].cpu().numpy().astype(np.float64)
+    assert not np.isnan(got).any()
+    rows = np.sort(np.random.default_rng(7).choice(n, 384, replace=False))
+    assert rel_err(got[:, rows], oracle.dense_f64(w[rows], x)) <= 1e-4
