@@ -818,26 +818,33 @@ static hipError_t prefill_cfg(const Launch& l0) {
     return hipGetLastError();
 }
 
-// The prefill workgroup shape (tokens x outputs; waves): the largest tile that still makes two waves per CU
-// (256 x 256 on 8 waves of 256 x 32, or 256 x 192 on 12 waves when that fills the CUs better; then 256 x 128 and
-// 128 x 128 on 4 waves), 64 x 128 for the smallest steps; QH_PF_SHAPE forces one in tuning sweeps.
+// The prefill workgroup shape (tokens x outputs; waves): 256 token rows (256 x 256 on 8 waves of 256 x 32, or 256 x 192
+// on 12 waves when that fills the CUs better), else 128 x 128 on 4 waves, else 64 x 128 on 4 waves; QH_PF_SHAPE forces
+// one in tuning sweeps (256 x 128 on 4 waves, 1, and the wider wave tiles 3 and 4 only then).
 template <int F, int EPI>
 static hipError_t prefill_epi(const Launch& l) {
     const int tiles = l.rows / TILE;
     auto items = [&](int bm, int wg_tiles) {
         return (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
     };
+    // token rows a tile height pads the step to, against the next smaller height (at most 15% more)
+    auto pads_ok = [&](int bm) {
+        const long h = bm / 2;
+        return (l.m + bm - 1) / bm * bm * 20 <= (l.m + h - 1) / h * h * 23;
+    };
+    // 256-token tiles want four waves per CU, or two where K is long (stream-K's fix-up amortised over 64+ groups);
+    // 128 x 128 tiles one (measured over M = 130..2048 on the 27B and 4B shapes)
+    const long waves2 = items(256, 16) * 8;
     int shape = l.pf_shape;
-    if (shape == 0) {  // enough waves: at least two per CU
-        if (l.m > 128 && items(256, 16) * 8 >= 2 * l.cus) {
+    if (shape == 0) {
+        if (l.m > 128 && (waves2 >= 4 * l.cus || (waves2 >= 2 * l.cus && l.cols / QG >= 64)) && pads_ok(256)) {
             shape = 2;
             // 256 x 192 on 12 waves when its rounds fill the CUs enough better to outweigh its lower rate (items of
             // 3/4 the work at about 0.85 of the rate of 256 x 256: (5120, 6144) at 2048 tokens fills all 256 CUs with
             // it, 3/4 of them with 256 x 256, measured +10%)
             Launch a = l, b = l;
             if (prefill_plan<F, EPI, 4, 1, 2, 6>(a) * 15 < prefill_plan<F, EPI, 8, 1, 1, 8>(b) * 17) shape = 7;
-        } else if (l.m > 128 && items(256, 8) * 4 >= 2 * l.cus) shape = 1;
-        else if (l.m > 64 && items(128, 8) * 4 >= 2 * l.cus) shape = 5;
+        } else if (l.m > 64 && items(128, 8) * 4 >= l.cus && pads_ok(128)) shape = 5;
         else shape = 6;
     }
     switch (shape) {

@@ -1,8 +1,8 @@
 """Parity of the prefill kernel where the launcher spreads work items over the resident workgroups by groups of K
 (stream-K): items cut between workgroups are summed from partials by the last workgroup to finish its segment.
 
-The shapes are chosen so that the launcher's cost rule picks stream-K: (m, 4096, 4096) at m = 130 and 256 run 64 x 128
-items (96 or 128 of them, fewer than one round) and pick it at any occupancy of 1-8 workgroups per CU; (512, 17408,
+The shapes are chosen so that the launcher's cost rule picks stream-K: (m, 4096, 4096) runs 96 items of 64 x 128 at
+m = 130 and 64 of 128 x 128 at m = 256, fewer than one round at any occupancy of 1-8 workgroups per CU; (512, 17408,
 5120) runs 136 items of 256 x 256 at the one workgroup per CU that shape holds. Same bar as the other prefill tests:
 the oracle to 2e-2 RMS, and the kernel's own arithmetic (bf16-rounded weights, exact f64 sums) to 1e-4.
 """
