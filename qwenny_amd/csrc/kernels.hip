@@ -777,14 +777,14 @@ static long prefill_plan(Launch& l) {
     const int tiles = l.rows / TILE, G = l.cols / QG;
     const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32, threads = WM * WN * 64;
     const long items = (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
-    static int per_cu = -1;  // resident workgroups per CU (per instantiation; the same on every MI355X)
-    if (per_cu < 0) {
+    // resident workgroups per CU (per instantiation; the same on every MI355X; thread-safe static initialisation)
+    static const int per_cu = [threads] {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>, threads,
                                                          0) != hipSuccess)
             n = 0;
-        per_cu = n;
-    }
+        return n;
+    }();
     const long P = (long)per_cu * l.cus;
     l.dp_items = (int)items;
     l.sk_items = 0;
