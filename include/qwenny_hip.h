@@ -210,6 +210,21 @@ int qh_sum_parts(void* stream, const float* x, int splits, size_t n, size_t ld, 
 int qh_add_rmsnorm(void* stream, float* h, const float* x, int splits, size_t n, size_t hidden, const float* w_next,
                    void* y_bf16, float eps);
 
+/* The LoRA consumers (kernels/lora.cuh:52-113, launched by src/cuda/qwen/lora.rs:143-190): an unmerged adapter adds
+ * s_t * B (A x) to a plain product for the tokens t whose slot uses it (s_t = slot_scale[tok_slot[t]]; 0: nothing
+ * added). xa: the stacked A product's partials f32 [split][n][m_cols] (m_cols <= 256); b_f16: B f16 [rows][rank] in
+ * the product's row order (rank 8, 16, 32 or 64; 16-byte aligned); tab: 8 int32, each module's end row (ascending;
+ * unused INT_MAX), then its first column of xa (-1: not adapted). All pointers are device addresses.
+ * lora_add: y [n][ldy] f32, the plain product's split 0, row o += s_t * B[o] . xa[t][off(o) ..].
+ * lora_silu: y [n][ldy] f32, a plain [gate; up] product packed in row_order(rows, 1) (split 1), read; mid [n][rows / 2]
+ * bf16 = silu(gate + delta) * (up + delta) for every token t < n, as the SwiGLU epilogue writes it (rows % 16 == 0).
+ * Launch only. */
+int qh_lora_add(void* stream, const float* xa, int split, int m_cols, const uint16_t* b_f16, int rank, size_t rows,
+                const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n, float* y, size_t ldy);
+int qh_lora_silu(void* stream, const float* xa, int split, int m_cols, const uint16_t* b_f16, int rank, size_t rows,
+                 const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n, const float* y,
+                 size_t ldy, void* mid_bf16);
+
 #ifdef __cplusplus
 }
 #endif

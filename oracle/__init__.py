@@ -180,6 +180,52 @@ def add_rmsnorm(h, x, splits, w_next, eps):
     return v, np.asarray(w_next, np.float64) * (d * r)
 
 
+def _lora_delta(xa, split, b_f16, rank, tab, tok_slot, slot_scale, n, rows_of):
+    """kernels/lora.cuh:13-46: per token the slot's scale s_t (0: no delta), xa summed over the splits (f32, split 0
+    first), and for output row o of module mod(o) (tab[0..3] end rows) with first column off = tab[4 + mod] >= 0 the
+    delta s_t * B[o] . xa[t][off .. off + rank) (f64 here). Returns (delta f64 [n][len(rows_of)], scales f32 [n])."""
+    xa = np.asarray(xa, np.float32)
+    m = xa.shape[-1]
+    xs = np.zeros((n, m), np.float32)
+    for s in range(split):
+        xs = xs + xa[s, :n]
+    sc = np.asarray(slot_scale, np.float32)[np.asarray(tok_slot)[:n]]
+    b = np.asarray(b_f16, np.uint16).view(np.float16).astype(np.float64).reshape(-1, rank)
+    delta = np.zeros((n, len(rows_of)), np.float64)
+    for i, o in enumerate(rows_of):
+        mod = int(o >= tab[0]) + int(o >= tab[1]) + int(o >= tab[2])
+        off = tab[4 + mod]
+        if off < 0:
+            continue
+        delta[:, i] = xs[:, off:off + rank].astype(np.float64) @ b[o]
+    return delta * sc[:, None].astype(np.float64), sc
+
+
+def lora_add(y, xa, split, b_f16, rank, tab, tok_slot, slot_scale, n):
+    """kernels/lora.cuh:52-76 (lora_add): y [n][rows] (a plain product's split 0) + s_t B (A x) for the tokens of
+    adapter slots; f64."""
+    y = np.asarray(y, np.float64)
+    delta, sc = _lora_delta(xa, split, b_f16, rank, tab, tok_slot, slot_scale, n, range(y.shape[1]))
+    return np.where(sc[:, None] != 0, y[:n] + delta, y[:n])
+
+
+def lora_silu(y, xa, split, b_f16, rank, tab, tok_slot, slot_scale, n):
+    """kernels/lora.cuh:78-113 (lora_silu): y [n][rows] a plain [gate; up] product packed in the SwiGLU row order
+    (16-row tile p: gate rows 8p .. 8p + 7, then their up rows); mid [n][rows / 2] = silu(gate + dg) * (up + du) in
+    f64, output j from packed rows 16 (j / 8) + j % 8 and + 8. Only tab[4] (gate) and tab[5] (up) are read."""
+    y = np.asarray(y, np.float64)[:n]
+    rows = y.shape[1]
+    j = np.arange(rows // 2)
+    og = 16 * (j // 8) + j % 8
+    ou = og + 8
+    t8 = [2**31 - 1] * 4 + [tab[4], -1, -1, -1]
+    dg, sc = _lora_delta(xa, split, b_f16, rank, t8, tok_slot, slot_scale, n, og)
+    t8 = [2**31 - 1] * 4 + [tab[5], -1, -1, -1]
+    du, _ = _lora_delta(xa, split, b_f16, rank, t8, tok_slot, slot_scale, n, ou)
+    g, u = y[:, og] + dg, y[:, ou] + du
+    return g / (1.0 + np.exp(-g)) * u
+
+
 # ---- epilogues (numpy restatements) ---------------------------------------------------------------------------
 
 

@@ -46,6 +46,8 @@ SIGNATURES = {
     "qh_dequant": (I, [P, P, P, P, S, S, S, I, I, S, S, P, I]),
     "qh_sum_parts": (I, [P, P, I, S, S, P]),
     "qh_add_rmsnorm": (I, [P, P, P, I, S, S, P, P, ctypes.c_float]),
+    "qh_lora_add": (I, [P, P, I, I, P, I, S, P, P, P, S, P, S]),
+    "qh_lora_silu": (I, [P, P, I, I, P, I, S, P, P, P, S, P, S, P]),
     "qh_pack_dense_bf16": (I, [P, S, S, P, S, P]),
     "qh_unpack_row_bf16": (I, [S, S, P, S, P]),
     "qh_mat_free": (None, [P]),

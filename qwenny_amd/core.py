@@ -370,6 +370,20 @@ def add_rmsnorm(stream, h, x, splits, n, hidden, w_next, y, eps=1e-6):
     check(lib().qh_add_rmsnorm(_stream(stream), _ptr(h), _ptr(x), splits, n, hidden, _ptr(w_next), _ptr(y), eps))
 
 
+def lora_add(stream, xa, split, m_cols, b_f16, rank, rows, tab, tok_slot, slot_scale, n, y, ldy=0):
+    """An unmerged LoRA adapter's delta on a plain product (kernels/lora.cuh:52-76, src/cuda/qwen/lora.rs:178-180):
+    y [n][ldy] (split 0) row o += s_t * B[o] . xa[t][off(o) ..] for the tokens of adapter slots; all device buffers."""
+    check(lib().qh_lora_add(_stream(stream), _ptr(xa), split, m_cols, _ptr(b_f16), rank, rows, _ptr(tab),
+                            _ptr(tok_slot), _ptr(slot_scale), n, _ptr(y), ldy or rows))
+
+
+def lora_silu(stream, xa, split, m_cols, b_f16, rank, rows, tab, tok_slot, slot_scale, n, y, mid, ldy=0):
+    """SwiGLU of a plain [gate; up] product with the adapter's delta added first (kernels/lora.cuh:78-113,
+    src/cuda/qwen/lora.rs:184-187): mid [n][rows / 2] bf16; all device buffers."""
+    check(lib().qh_lora_silu(_stream(stream), _ptr(xa), split, m_cols, _ptr(b_f16), rank, rows, _ptr(tab),
+                             _ptr(tok_slot), _ptr(slot_scale), n, _ptr(y), ldy or rows, _ptr(mid)))
+
+
 def pack_dense_bf16(w_bf16, order):
     """Dense bf16 rows `order` in the QH_WT_BF16 tile layout (src/cuda/core.rs:370-381, kept bf16) -> codes bytes."""
     w = np.ascontiguousarray(w_bf16, np.uint16)

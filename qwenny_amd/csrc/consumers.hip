@@ -1,7 +1,8 @@
 // Consumers of the plain products' split-K partials (the output contract y [split][n][ld] f32): the reference's
 // sum_parts (kernels/qwen.cu:141-143, part_sum kernels/common.cuh:66-70) and add_rmsnorm (kernels/qwen.cu:57-80),
-// the residual step after the o_proj / out_proj / down products. HBM-bound; f32 sums in the reference's order
-// (h + x[0], then x[1], x[2], ..), so the sums are bit-identical to it.
+// the residual step after the o_proj / out_proj / down products, and the LoRA epilogue (kernels/lora.cuh) that adds an
+// unmerged adapter's delta to them. HBM-bound; f32 sums in the reference's order (h + x[0], then x[1], x[2], ..), so
+// the sums are bit-identical to it.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -61,7 +62,178 @@ __global__ __launch_bounds__(AR_THREADS) void add_rmsnorm_kernel(float* __restri
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// LoRA consumers (kernels/lora.cuh:52-113, launched by src/cuda/qwen/lora.rs:143-190): an unmerged adapter adds
+// s_t B (A x) to a plain product for the tokens t of the slots that use it. A x arrives as the split-K partials xa
+// [split][n][M] of the stacked A product (M = adapted modules x rank, at most 256 columns); B is f16 [rows][R] in the
+// product's row order; tab (8 ints) holds each module's end row (ascending; unused INT_MAX), then its first column of
+// xa (-1: not adapted). A workgroup takes LORA_TT tokens and 256 rows (add) or 256 SwiGLU outputs (silu): the tokens'
+// scales and their xa (the partials summed in split order) are staged in LDS once, each thread reads its B row as
+// 16-byte loads and dots it with the staged xa in f32, in column order.
+
+constexpr int LORA_TT = 8;
+constexpr int LORA_MAXM = 256;
+
+struct LoraArgs {
+    const float* xa;
+    int split, M;
+    const uint16_t* b;
+    int rows;
+    const int* tab;
+    const int* tok_slot;
+    const float* slot_scale;
+    int n;
+    int ldy;
+};
+
+// the block's token scales (0 past n) and, for the tokens with a nonzero scale, xa summed over the splits
+__device__ void lora_stage(const LoraArgs& a, int t0, float (*xs)[LORA_MAXM], float* sc) {
+    if (threadIdx.x < LORA_TT) {
+        const int t = t0 + threadIdx.x;
+        sc[threadIdx.x] = t < a.n ? a.slot_scale[a.tok_slot[t]] : 0.0f;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < LORA_TT * a.M; i += blockDim.x) {
+        const int tl = i / a.M, c = i - tl * a.M, t = t0 + tl;
+        float v = 0.0f;
+        if (sc[tl] != 0.0f)
+            for (int s = 0; s < a.split; s++) v += a.xa[((size_t)s * a.n + t) * a.M + c];
+        xs[tl][c] = v;
+    }
+    __syncthreads();
+}
+
+// B row o (f16 [R]) as f32
+template <int R>
+__device__ __forceinline__ void lora_b_row(const uint16_t* b, int o, float (&w)[R]) {
+    const uint4* p = (const uint4*)(b + (size_t)o * R);
+#pragma unroll
+    for (int i = 0; i < R / 8; i++) {
+        const uint4 u = p[i];
+        const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            w[8 * i + 2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h[k] & 0xffffu));
+            w[8 * i + 2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h[k] >> 16));
+        }
+    }
+}
+
+template <int R>
+__device__ __forceinline__ float lora_dot(const float (&w)[R], const float* x) {
+    float d = 0.0f;
+#pragma unroll
+    for (int j = 0; j < R; j++) d = __builtin_fmaf(w[j], x[j], d);
+    return d;
+}
+
+// y [n][ldy] (a plain product's split 0) row o += s_t B[o] . xa[t][off(o) ..] for the adapter tokens
+template <int R>
+__global__ __launch_bounds__(256) void lora_add_kernel(LoraArgs a, float* __restrict__ y) {
+    __shared__ float xs[LORA_TT][LORA_MAXM];
+    __shared__ float sc[LORA_TT];
+    const int t0 = blockIdx.y * LORA_TT;
+    lora_stage(a, t0, xs, sc);
+    bool any = false;
+#pragma unroll
+    for (int i = 0; i < LORA_TT; i++) any |= sc[i] != 0.0f;
+    const int o = blockIdx.x * 256 + threadIdx.x;
+    if (!any || o >= a.rows) return;
+    const int mod = (o >= a.tab[0]) + (o >= a.tab[1]) + (o >= a.tab[2]), off = a.tab[4 + mod];
+    if (off < 0) return;
+    float w[R];
+    lora_b_row<R>(a.b, o, w);
+#pragma unroll
+    for (int tl = 0; tl < LORA_TT; tl++)
+        if (sc[tl] != 0.0f) {
+            float* yo = y + (size_t)(t0 + tl) * a.ldy + o;
+            *yo = __builtin_fmaf(sc[tl], lora_dot<R>(w, &xs[tl][off]), *yo);
+        }
+}
+
+// mid [n][rows / 2] (bf16) = SwiGLU of the plain [gate; up] product y [n][ldy] (split 1, packed in the SwiGLU
+// epilogue's row order: 16-row tile p holds gate rows 8p .. 8p + 7, then their up rows) with the delta added first
+template <int R>
+__global__ __launch_bounds__(256) void lora_silu_kernel(LoraArgs a, const float* __restrict__ y, __bf16* mid) {
+    __shared__ float xs[LORA_TT][LORA_MAXM];
+    __shared__ float sc[LORA_TT];
+    const int t0 = blockIdx.y * LORA_TT;
+    lora_stage(a, t0, xs, sc);
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= a.rows / 2) return;
+    const int og = 16 * (j / 8) + j % 8, ou = og + 8, offg = a.tab[4], offu = a.tab[5];
+    float wg[R], wu[R];
+    if (offg >= 0) lora_b_row<R>(a.b, og, wg);
+    if (offu >= 0) lora_b_row<R>(a.b, ou, wu);
+    for (int tl = 0; tl < LORA_TT && t0 + tl < a.n; tl++) {
+        const size_t r = (size_t)(t0 + tl) * a.ldy;
+        float g = y[r + og], u = y[r + ou];
+        if (sc[tl] != 0.0f) {
+            if (offg >= 0) g = __builtin_fmaf(sc[tl], lora_dot<R>(wg, &xs[tl][offg]), g);
+            if (offu >= 0) u = __builtin_fmaf(sc[tl], lora_dot<R>(wu, &xs[tl][offu]), u);
+        }
+        mid[(size_t)(t0 + tl) * (a.rows / 2) + j] = (__bf16)(g / (1.0f + __expf(-g)) * u);
+    }
+}
+
+int lora_launch(void* stream, const LoraArgs& a, int rank, float* y_add, const float* y_silu, __bf16* mid) {
+    const bool silu = mid != nullptr;
+    const unsigned per = 256, outs = (unsigned)(silu ? a.rows / 2 : a.rows);
+    const dim3 grid((outs + per - 1) / per, (unsigned)((a.n + LORA_TT - 1) / LORA_TT));
+    hipStream_t s = (hipStream_t)stream;
+#define QH_LORA_CASE(R)                                                                      \
+    case R:                                                                                  \
+        if (silu)                                                                            \
+            hipLaunchKernelGGL(lora_silu_kernel<R>, grid, dim3(256), 0, s, a, y_silu, mid);  \
+        else                                                                                 \
+            hipLaunchKernelGGL(lora_add_kernel<R>, grid, dim3(256), 0, s, a, y_add);         \
+        break;
+    switch (rank) {
+        QH_LORA_CASE(8)
+        QH_LORA_CASE(16)
+        QH_LORA_CASE(32)
+        QH_LORA_CASE(64)
+        default: return fail(QH_EINVAL, "LoRA rank %d: ranks 8, 16, 32 and 64 are served", rank);
+    }
+#undef QH_LORA_CASE
+    if (hipError_t e = hipGetLastError(); e != hipSuccess)
+        return fail(QH_EHIP, "lora launch: %s", hipGetErrorString(e));
+    return QH_OK;
+}
+
+int lora_check(const float* xa, int split, int m_cols, const uint16_t* b, size_t rows, const int32_t* tab,
+               const int32_t* tok_slot, const float* slot_scale, size_t n, const void* y, size_t ldy, bool silu) {
+    if (!xa || !b || !tab || !tok_slot || !slot_scale || !y || split < 1)
+        return fail(QH_EINVAL, "lora: null or %d splits", split);
+    if (m_cols < 1 || m_cols > LORA_MAXM)
+        return fail(QH_EINVAL, "lora: %d columns of xa (at most %d)", m_cols, LORA_MAXM);
+    if (rows == 0 || rows > (1u << 30) || n > (1u << 24) || ldy < rows || ldy > (1u << 30) || (uintptr_t)b % 16 ||
+        (silu && rows % 16))
+        return fail(QH_EINVAL, "lora: %zu rows (ld %zu), %zu tokens, B 16-byte aligned%s", rows, ldy, n,
+                    silu ? ", rows a multiple of 16" : "");
+    return QH_OK;
+}
+
 }  // namespace
+
+extern "C" int qh_lora_add(void* stream, const float* xa, int split, int m_cols, const uint16_t* b_f16, int rank,
+                           size_t rows, const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n,
+                           float* y, size_t ldy) {
+    if (n == 0) return QH_OK;
+    if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy, false)) return e;
+    const LoraArgs a{xa, split, m_cols, b_f16, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
+    return lora_launch(stream, a, rank, y, nullptr, nullptr);
+}
+
+extern "C" int qh_lora_silu(void* stream, const float* xa, int split, int m_cols, const uint16_t* b_f16, int rank,
+                            size_t rows, const int32_t* tab, const int32_t* tok_slot, const float* slot_scale,
+                            size_t n, const float* y, size_t ldy, void* mid_bf16) {
+    if (n == 0) return QH_OK;
+    if (!mid_bf16) return fail(QH_EINVAL, "lora silu: null output");
+    if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy, true)) return e;
+    const LoraArgs a{xa, split, m_cols, b_f16, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
+    return lora_launch(stream, a, rank, nullptr, y, (__bf16*)mid_bf16);
+}
 
 extern "C" int qh_sum_parts(void* stream, const float* x, int splits, size_t n, size_t ld, float* y) {
     if (n == 0 || ld == 0) return QH_OK;

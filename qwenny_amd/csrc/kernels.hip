@@ -778,7 +778,7 @@ static long prefill_plan(Launch& l) {
     const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32, threads = WM * WN * 64;
     const long items = (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
     // resident workgroups per CU (per instantiation; the same on every MI355X; thread-safe static initialisation)
-    static const int per_cu = [threads] {
+    static const int per_cu = [] {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>, threads,
                                                          0) != hipSuccess)

@@ -326,3 +326,72 @@ def test_add_rmsnorm_closed_form():
     hn, y = oracle.add_rmsnorm(np.zeros((1, 2), np.float32), np.array([[[1.0, 2.0]], [[2.0, 2.0]]], np.float32), 2,
                                w, 0.0)
     assert np.array_equal(hn, h) and np.allclose(y, [[2 * 3 / np.sqrt(12.5), 0.5 * 4 / np.sqrt(12.5)]], rtol=1e-12)
+
+
+# ---- LoRA consumers (kernels/lora.cuh) --------------------------------------------------------------------------
+
+
+def _lora_case(seed, n=5, split=3, rank=8, m_cols=32):
+    rng = np.random.default_rng(seed)
+    xa = rng.standard_normal((split, n, m_cols)).astype(np.float32)
+    slot_scale = np.array([0.0, 0.5, 2.0], np.float32)
+    tok_slot = rng.integers(0, 3, n).astype(np.int32)
+    return xa, slot_scale, tok_slot
+
+
+def test_lora_add_one_hot_rows():
+    """B[o] = e_(o % rank) makes the delta s_t * sum_s xa[s][t][off + o % rank]: a closed form."""
+    n, split, rank, rows = 6, 3, 8, 32
+    xa, slot_scale, tok_slot = _lora_case(1, n, split, rank)
+    b = np.zeros((rows, rank), np.float16)
+    b[np.arange(rows), np.arange(rows) % rank] = 1.0
+    tab = [2**31 - 1] * 4 + [8, -1, -1, -1]
+    y = np.random.default_rng(2).standard_normal((n, rows)).astype(np.float32)
+    got = oracle.lora_add(y, xa, split, b.view(np.uint16), rank, tab, tok_slot, slot_scale, n)
+    xs = xa.astype(np.float64).sum(0)
+    want = y + slot_scale[tok_slot][:, None] * xs[:, 8 + np.arange(rows) % rank]
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+    assert (got[slot_scale[tok_slot] == 0] == y[slot_scale[tok_slot] == 0]).all()
+
+
+def test_lora_add_module_routing():
+    """Three stacked modules (end rows 16, 48, 64): the first reads xa columns 0.., the second is not adapted, the third
+    reads columns 8..; each equals the dense s * B_m (A x) of its own module."""
+    n, split, rank = 4, 2, 8
+    xa, slot_scale, tok_slot = _lora_case(3, n, split, rank, 16)
+    rng = np.random.default_rng(4)
+    b = rng.standard_normal((64, rank)).astype(np.float16)
+    tab = [16, 48, 2**31 - 1, 2**31 - 1, 0, -1, 8, -1]
+    y = np.zeros((n, 64), np.float32)
+    got = oracle.lora_add(y, xa, split, b.view(np.uint16), rank, tab, tok_slot, slot_scale, n)
+    xs = xa.astype(np.float64).sum(0)
+    s = slot_scale[tok_slot].astype(np.float64)[:, None]
+    assert np.allclose(got[:, :16], s * (xs[:, 0:8] @ b[:16].astype(np.float64).T))
+    assert (got[:, 16:48] == 0).all()
+    assert np.allclose(got[:, 48:], s * (xs[:, 8:16] @ b[48:].astype(np.float64).T))
+
+
+def test_lora_silu_matches_swiglu_of_the_sum():
+    """lora_silu = the SwiGLU epilogue (silu_glu over row_order's packing) of the plain product plus lora_add's delta."""
+    from qwenny_amd import row_order
+
+    n, split, rank, rows = 5, 2, 16, 64
+    xa, slot_scale, tok_slot = _lora_case(5, n, split, rank, 32)
+    rng = np.random.default_rng(6)
+    b = rng.standard_normal((rows, rank)).astype(np.float16)  # rows in the packed (product) order
+    tab = [2**31 - 1] * 4 + [0, 16, -1, -1]
+    y = rng.standard_normal((n, rows)).astype(np.float32)  # packed order
+    got = oracle.lora_silu(y, xa, split, b.view(np.uint16), rank, tab, tok_slot, slot_scale, n)
+    # the same delta through lora_add, module 0 = packed gate rows, module 1 = packed up rows
+    order = row_order(rows, True)  # packed row i <- original row order[i]
+    gate_rows = np.flatnonzero(order < rows // 2)
+    up_rows = np.flatnonzero(order >= rows // 2)
+    full = np.zeros((n, rows), np.float64)
+    for rows_m, off in ((gate_rows, 0), (up_rows, 16)):
+        bm = np.zeros_like(b)
+        bm[rows_m] = b[rows_m]
+        t = [2**31 - 1] * 4 + [off, -1, -1, -1]
+        full += oracle.lora_add(np.zeros_like(y), xa, split, bm.view(np.uint16), rank, t, tok_slot, slot_scale, n)
+    orig = np.empty_like(full)
+    orig[:, order] = y + full  # back to original order [gate; up]
+    assert np.allclose(got, oracle.silu_glu(orig, None), rtol=1e-9, atol=1e-9)
