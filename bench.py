@@ -313,6 +313,66 @@ def dequant_line(args):
     return {"dequant_i4_to_bf16_GBps": gbs}
 
 
+def consumers_line(args):
+    """The partials consumers and the LoRA epilogue at 27B sizes, after the down projection (K 17408 -> 5120 rows) and
+    on [gate; up] (34816 rows, rank 16): M = 1 (34 split-K partials) and M = 2048 (one). HBM GB/s over the bytes each
+    reads and writes once; microseconds per launch (these launches are short: the launch and its ramp dominate)."""
+    import torch
+
+    from qwenny_amd import add_rmsnorm, lora_add, lora_silu, sum_parts
+
+    out = {}
+    hid, gu, rank, mcols = 5120, 34816, 16, 64
+    g = torch.Generator(device="cuda").manual_seed(7)
+    b = (torch.randn(gu, rank, device="cuda", generator=g) * 0.05).half().view(torch.int16)
+    tab_add = torch.tensor([2**31 - 1] * 4 + [0, -1, -1, -1], dtype=torch.int32, device="cuda")
+    tab_silu = torch.tensor([2**31 - 1] * 4 + [0, rank, -1, -1], dtype=torch.int32, device="cuda")
+    scale = torch.tensor([1.0], dtype=torch.float32, device="cuda")
+    for m, split in ((1, 34), (2048, 1)):
+        x = torch.randn(split, m, hid, device="cuda", generator=g)
+        h = torch.randn(m, hid, device="cuda", generator=g)
+        w = torch.ones(hid, device="cuda")
+        yb = torch.empty(m, hid, dtype=torch.bfloat16, device="cuda")
+        ys = torch.empty(m, hid, device="cuda")
+        xa = torch.randn(1, m, mcols, device="cuda", generator=g)
+        slot = torch.zeros(m, dtype=torch.int32, device="cuda")
+        ygu = torch.randn(m, gu, device="cuda", generator=g)
+        mid = torch.empty(m, gu // 2, dtype=torch.bfloat16, device="cuda")
+        cases = {
+            "sum_parts": (lambda: sum_parts(None, x, split, m, hid, ys), (split + 1) * m * hid * 4),
+            "add_rmsnorm": (lambda: add_rmsnorm(None, h, x, split, m, hid, w, yb),
+                            (split + 2) * m * hid * 4 + hid * 4 + m * hid * 2),
+            "lora_add": (lambda: lora_add(None, xa, 1, mcols, b, rank, hid, tab_add, slot, scale, m, ys),
+                         m * mcols * 4 + hid * rank * 2 * -(-m // 8) + 2 * m * hid * 4),
+            "lora_silu": (lambda: lora_silu(None, xa, 1, mcols, b, rank, gu, tab_silu, slot, scale, m, ygu, mid),
+                          m * mcols * 4 + gu * rank * 2 * -(-m // 8) + m * gu * 4 + m * gu),
+        }
+        for name, (fn, nbytes) in cases.items():
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            # 20 launches per HIP graph, replayed: the kernels' own time plus the graph's per-launch cost
+            graph, st = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+            with torch.cuda.stream(st):
+                with torch.cuda.graph(graph, stream=st):
+                    for _ in range(20):
+                        fn()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            reps = 10
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(reps):
+                graph.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            s = t0.elapsed_time(t1) / (reps * 20) * 1e-3
+            out[f"{name}_m{m}"] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 1)}
+            print(f"# {name} M={m}: {s * 1e6:.2f} us, {nbytes / s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+    return {"consumers": out}
+
+
 def summarize_clock(pmc_dir, min_ns=50000):
     """Per kernel (name, grid) of a rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: mean duration, the
     clock it ran at (GRBM_GUI_ACTIVE sums the 8 XCDs' cycles) and the fraction of cycles each SIMD's MFMA unit was busy
@@ -350,7 +410,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant")
+    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant,consumers (the last only when named)")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -477,6 +537,8 @@ def main():
         extra.update(dense_lines(gemm, args))
     if "dequant" in only:
         extra.update(dequant_line(args))
+    if "consumers" in only:
+        extra.update(consumers_line(args))
 
     line = {
         "metric": "int4 GEMM HBM GB/s (% of 8 TB/s) at M=1/5; TFLOP/s (% bf16 MFMA peak) at M=2048",

@@ -13,35 +13,89 @@ using namespace qh;
 
 namespace {
 
-// y [n][ld] = sum over s of x [s][n][ld]; one thread per 4 columns (ld % 4 == 0), grid-stride over n * ld / 4
-__global__ __launch_bounds__(256) void sum_parts_kernel(const float4* __restrict__ x, int splits, long n4, float4* y) {
-    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int s = 0; s < splits; s++) {
-            const float4 p = x[(size_t)s * n4 + i];
-            v.x += p.x, v.y += p.y, v.z += p.z, v.w += p.w;
-        }
-        y[i] = v;
+// v += x[0][i] + x[1][i] + .. + x[splits - 1][i], in that order; the partials load 8 at a time ahead of their adds
+// (the sum of 34 partials of a decode product is then 5 memory round trips, not 34)
+__device__ __forceinline__ void add_splits(float4& v, const float4* __restrict__ x, int splits, long n4, long i) {
+    constexpr int B = 8;
+    for (int s0 = 0; s0 < splits; s0 += B) {
+        float4 p[B];
+#pragma unroll
+        for (int j = 0; j < B; j++)
+            if (s0 + j < splits) p[j] = x[(size_t)(s0 + j) * n4 + i];
+#pragma unroll
+        for (int j = 0; j < B; j++)
+            if (s0 + j < splits) v.x += p[j].x, v.y += p[j].y, v.z += p[j].z, v.w += p[j].w;
+    }
+}
+
+// y [n][ld] = sum over s of x [s][n][ld] (from 0; h = nullptr), or h [n][ld] += that sum (h + x[0] first, as the
+// residual step adds); one thread per 4 columns (ld % 4 == 0), grid-stride over n * ld / 4
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float4* __restrict__ x, int splits, long n4, float4* y,
+                                                        float4* h) {
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
+        float4 v = h ? h[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        add_splits(v, x, splits, n4, i);
+        (h ? h : y)[i] = v;
     }
 }
 
 constexpr int AR_THREADS = 256;
+// add_rmsnorm spreads the partials' sum over workgroups below this many float4 per step (n * hidden / 4): 64 tokens
+// of a 5120-wide row, where a workgroup per token leaves most CUs idle
+constexpr long AR_SPREAD_BELOW = 64l * 1280;
 
-// token t (one workgroup): h[t] += the sum of the partials x[.][t]; y[t] = bf16(w * (h[t] / rms(h[t])))
-__global__ __launch_bounds__(AR_THREADS) void add_rmsnorm_kernel(float* __restrict__ h, const float* __restrict__ x,
-                                                                 int splits, int n, int H, const float* __restrict__ w,
-                                                                 __bf16* __restrict__ y, float eps) {
-    __shared__ float wsum[AR_THREADS / 64];
+// y[t] = bf16(w * (h[t] / rms(h[t]))) with the row held in registers: each of the T threads loads its C float4 of h
+// and of w at once (one memory round trip), then the sum of squares and the output (H4 <= T * C)
+template <int T, int C>
+__global__ __launch_bounds__(T) void rmsnorm_kernel(const float* __restrict__ h, int H, const float* __restrict__ w,
+                                                    __bf16* __restrict__ y, float eps) {
+    __shared__ float wsum[T / 64];
+    const size_t base = (size_t)blockIdx.x * H;
+    const int H4 = H / 4;
+    float4 v[C], wn[C];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        const int c = threadIdx.x + i * T;
+        v[i] = c < H4 ? ((const float4*)(h + base))[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        wn[i] = c < H4 ? ((const float4*)w)[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < C; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < T / 64; i++) tot += wsum[i];
+    const float r = rsqrtf(tot / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        const int c = threadIdx.x + i * T;
+        if (c >= H4) break;
+        __bf16* yo = y + base + 4 * c;
+        yo[0] = (__bf16)(wn[i].x * (v[i].x * r));
+        yo[1] = (__bf16)(wn[i].y * (v[i].y * r));
+        yo[2] = (__bf16)(wn[i].z * (v[i].z * r));
+        yo[3] = (__bf16)(wn[i].w * (v[i].w * r));
+    }
+}
+
+// token t (one workgroup of T threads): h[t] += the sum of the partials x[.][t]; y[t] = bf16(w * (h[t] / rms(h[t])))
+template <int T>
+__global__ __launch_bounds__(T) void add_rmsnorm_kernel(float* __restrict__ h, const float* __restrict__ x, int splits,
+                                                        int n, int H, const float* __restrict__ w,
+                                                        __bf16* __restrict__ y, float eps) {
+    __shared__ float wsum[T / 64];
     const size_t base = (size_t)blockIdx.x * H;
     const int H4 = H / 4;
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < H4; c += AR_THREADS) {
+    for (int c = threadIdx.x; c < H4; c += T) {
         float4 v = ((const float4*)(h + base))[c];
-        for (int s = 0; s < splits; s++) {
-            const float4 p = ((const float4*)(x + (size_t)s * n * H + base))[c];
-            v.x += p.x, v.y += p.y, v.z += p.z, v.w += p.w;
+        if (splits) {
+            add_splits(v, (const float4*)x, splits, (long)n * H4, (long)blockIdx.x * H4 + c);
+            ((float4*)(h + base))[c] = v;
         }
-        ((float4*)(h + base))[c] = v;
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
@@ -49,10 +103,10 @@ __global__ __launch_bounds__(AR_THREADS) void add_rmsnorm_kernel(float* __restri
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
-    for (int i = 0; i < AR_THREADS / 64; i++) tot += wsum[i];
+    for (int i = 0; i < T / 64; i++) tot += wsum[i];
     const float r = rsqrtf(tot / (float)H + eps);
     // the second pass re-reads this workgroup's own h row (written above by the same threads, same columns)
-    for (int c = threadIdx.x; c < H4; c += AR_THREADS) {
+    for (int c = threadIdx.x; c < H4; c += T) {
         const float4 v = ((const float4*)(h + base))[c], wn = ((const float4*)w)[c];
         __bf16* yo = y + base + 4 * c;
         yo[0] = (__bf16)(wn.x * (v.x * r));
@@ -235,17 +289,22 @@ extern "C" int qh_lora_silu(void* stream, const float* xa, int split, int m_cols
     return lora_launch(stream, a, rank, nullptr, y, (__bf16*)mid_bf16);
 }
 
+// launch sum_parts_kernel over n4 float4: workgroups of 64 threads for decode-sized rows (one float4 per thread over
+// 4x as many CUs), 256 otherwise
+static int sum_launch(hipStream_t s, const float* x, int splits, long n4, float* y, float* h) {
+    const unsigned t = n4 < 64l * 1024 ? 64 : 256, blocks = (unsigned)std::min<long>((n4 + t - 1) / t, 4096);
+    hipLaunchKernelGGL(sum_parts_kernel, dim3(blocks), dim3(t), 0, s, (const float4*)x, splits, n4, (float4*)y,
+                       (float4*)h);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_EHIP;
+}
+
 extern "C" int qh_sum_parts(void* stream, const float* x, int splits, size_t n, size_t ld, float* y) {
     if (n == 0 || ld == 0) return QH_OK;
     if (!x || !y || splits < 1) return fail(QH_EINVAL, "sum_parts: null or %d splits", splits);
     if (ld % 4 || (uintptr_t)x % 16 || (uintptr_t)y % 16)
         return fail(QH_EINVAL, "sum_parts: rows of %zu floats must be a multiple of 4, buffers 16-byte aligned", ld);
-    const long n4 = (long)(n * ld / 4);
-    const unsigned blocks = (unsigned)std::min<long>((n4 + 255) / 256, 4096);
-    hipLaunchKernelGGL(sum_parts_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const float4*)x, splits, n4,
-                       (float4*)y);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess)
-        return fail(QH_EHIP, "sum_parts launch: %s", hipGetErrorString(e));
+    if (sum_launch((hipStream_t)stream, x, splits, (long)(n * ld / 4), y, nullptr))
+        return fail(QH_EHIP, "sum_parts launch failed");
     return QH_OK;
 }
 
@@ -256,8 +315,22 @@ extern "C" int qh_add_rmsnorm(void* stream, float* h, const float* x, int splits
     if (hidden == 0 || hidden % 4 || hidden > (1u << 24) || n > 0x7fffffffu || (uintptr_t)h % 16 ||
         (uintptr_t)x % 16 || (uintptr_t)w_next % 16)
         return fail(QH_EINVAL, "add_rmsnorm: hidden %zu must be a multiple of 4, f32 buffers 16-byte aligned", hidden);
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)n), dim3(AR_THREADS), 0, (hipStream_t)stream, h, x, splits,
-                       (int)n, (int)hidden, w_next, (__bf16*)y_bf16, eps);
+    // few tokens (decode): the partials' sum, the bulk of the bytes, over many workgroups first (a workgroup per token
+    // would read a 34-split partial set of a 5120-wide row alone, about 20 us), then the norm with no partials left
+    const long n4 = (long)(n * hidden / 4);
+    if (splits > 1 && (long)n * (hidden / 4) < (long)AR_SPREAD_BELOW) {
+        if (sum_launch((hipStream_t)stream, x, splits, n4, nullptr, h)) return fail(QH_EHIP, "add_rmsnorm launch failed");
+        // the norm alone, a wide workgroup per token with the row in registers
+        if (hidden / 4 <= 1024 * 4)
+            hipLaunchKernelGGL((rmsnorm_kernel<1024, 4>), dim3((unsigned)n), dim3(1024), 0, (hipStream_t)stream, h,
+                               (int)hidden, w_next, (__bf16*)y_bf16, eps);
+        else
+            hipLaunchKernelGGL(add_rmsnorm_kernel<1024>, dim3((unsigned)n), dim3(1024), 0, (hipStream_t)stream, h, x,
+                               0, (int)n, (int)hidden, w_next, (__bf16*)y_bf16, eps);
+    } else {
+        hipLaunchKernelGGL(add_rmsnorm_kernel<AR_THREADS>, dim3((unsigned)n), dim3(AR_THREADS), 0, (hipStream_t)stream,
+                           h, x, splits, (int)n, (int)hidden, w_next, (__bf16*)y_bf16, eps);
+    }
     if (hipError_t e = hipGetLastError(); e != hipSuccess)
         return fail(QH_EHIP, "add_rmsnorm launch: %s", hipGetErrorString(e));
     return QH_OK;
