@@ -31,7 +31,8 @@ def test_sum_parts(splits, n, ld):
     assert np.array_equal(y.cpu().numpy(), oracle.sum_parts(x, splits))
 
 
-@pytest.mark.parametrize("splits,n,hidden", [(1, 1, 2560), (10, 1, 5120), (34, 5, 5120), (1, 64, 1024)])
+@pytest.mark.parametrize("splits,n,hidden", [(1, 1, 2560), (10, 1, 5120), (34, 5, 5120), (1, 64, 1024), (3, 128, 5120),
+                                              (2, 1, 20480)])
 def test_add_rmsnorm(splits, n, hidden):
     import torch
 
