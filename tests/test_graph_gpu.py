@@ -83,3 +83,69 @@ def test_empty_step_launches_nothing(gemm):
     assert gemm.run(None, 0, mat, x, y, Epi.Plain) == 1
     torch.cuda.synchronize()
     assert (y.cpu().numpy() == 7.0).all()
+
+
+def test_graph_consumers_replay(gemm):
+    """The partials consumers and the LoRA epilogue captured after a decode product (add_rmsnorm's spread sum and
+    norm, sum_parts, lora_add, lora_silu), replayed with new partials: every replay equals the eager launches."""
+    import torch
+
+    from qwenny_amd import add_rmsnorm, lora_add, lora_silu, sum_parts
+
+    print("graph replays of the consumers", flush=True)
+    m, hid, split, rank, gu = 3, 5120, 34, 16, 1024
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.empty(split, m, hid, device="cuda")
+    h0 = torch.randn(m, hid, device="cuda", generator=g)
+    h = torch.empty_like(h0)
+    w = torch.rand(hid, device="cuda", generator=g) + 0.5
+    y = torch.empty(m, hid, dtype=torch.bfloat16, device="cuda")
+    s = torch.empty(m, hid, device="cuda")
+    xa = torch.empty(2, m, 32, device="cuda")
+    b = (torch.randn(gu, rank, device="cuda", generator=g) * 0.05).half().view(torch.int16)
+    tab = torch.tensor([512, 2**31 - 1, 2**31 - 1, 2**31 - 1, 0, 16, -1, -1], dtype=torch.int32, device="cuda")
+    tab_silu = torch.tensor([2**31 - 1] * 4 + [0, 16, -1, -1], dtype=torch.int32, device="cuda")
+    slot = torch.tensor([0, 1, 0], dtype=torch.int32, device="cuda")
+    scale = torch.tensor([0.5, 0.0], device="cuda")
+    ygu = torch.empty(m, gu, device="cuda")
+    ylo = torch.empty(m, gu, device="cuda")
+    mid = torch.empty(m, gu // 2, dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        h.copy_(h0)
+        add_rmsnorm(None, h, x, split, m, hid, w, y)
+        sum_parts(None, x, split, m, hid, s)
+        lora_add(None, xa, 2, 32, b, rank, gu, tab, slot, scale, m, ylo)
+        lora_silu(None, xa, 2, 32, b, rank, gu, tab_silu, slot, scale, m, ygu, mid)
+
+    def load(seed):
+        gg = torch.Generator(device="cuda").manual_seed(seed)
+        x.copy_(torch.randn(split, m, hid, device="cuda", generator=gg) * 0.3)
+        xa.copy_(torch.randn(2, m, 32, device="cuda", generator=gg))
+        ygu.copy_(torch.randn(m, gu, device="cuda", generator=gg))
+        ylo.copy_(torch.randn(m, gu, device="cuda", generator=gg))
+
+    outs = lambda: [t.float().cpu().numpy().copy() for t in (h, y, s, ylo, mid)]
+    load(1)
+    step()
+    torch.cuda.synchronize()
+    graph, st = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(graph, stream=st):
+            step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        load(10 + rep)
+        ylo_in = ylo.clone()
+        torch.cuda.synchronize()
+        step()
+        torch.cuda.synchronize()
+        want = outs()
+        ylo.copy_(ylo_in)
+        for t in (y, s, mid):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b_ in zip(outs(), want):
+            assert np.array_equal(a, b_), rep
