@@ -12,7 +12,9 @@
  *   Checkpoint::packed_matrix (:408-453), row_order (cuda/core.rs:108-114), Mat (:94-104),
  *   Mat::new / pack (:127-135, :338-389), Mat::marlin_rows (:140-153), Mat::marlin (:159-164), Mat::int8 (:168-191),
  *   part_len (:315-318), Gemm::load (:436-481), Gemm::run / run_split (:485-561), Gemm::put_block (:619-657),
- *   Gemm::block_stage (:675-680).
+ *   Gemm::block_stage (:675-680); the kernels the engine launches on the products' partials: add_rmsnorm and
+ *   sum_parts (kernels/qwen.cu:57-80, :141-143), the LoRA epilogue (kernels/lora.cuh:52-113); and the trainer's
+ *   dequant (kernels/qwen_train.cu:84-103).
  */
 #ifndef QWENNY_HIP_H
 #define QWENNY_HIP_H
@@ -31,7 +33,7 @@ extern "C" {
 #define QH_ENOMEM -3   /* device or host allocation failed */
 #define QH_ENOTFIT -4  /* the matrix does not fit this storage (e.g. non-integer zero points) */
 
-/* How a matrix is stored for the kernels (core.rs:65-79 `Wt`, without F16: dense 16-bit products are not built). */
+/* How a matrix is stored for the kernels (core.rs:65-79 `Wt`; its F16 is QH_WT_BF16 here). */
 enum qh_wt {
     QH_WT_I8 = 1,  /* int8 stored q + 128, an f32 scale per row and 128 columns (core.rs Wt::I8) */
     QH_WT_I4 = 2,  /* symmetric int4 (zero point 8), bf16 scale per row and 128 columns (core.rs Wt::Marlin) */
@@ -72,7 +74,7 @@ typedef struct qh_mat_desc {
     size_t valid;       /* rows that count for the argmax (core.rs Mat::valid) */
     size_t code_bytes;  /* device bytes of the packed codes */
     size_t scale_bytes; /* device bytes of the scales */
-    size_t zero_bytes;  /* device bytes of the zero points (0 unless QH_WT_I4Z) */
+    size_t zero_bytes;  /* device bytes of the zero points (0 unless QH_WT_I4Z or QH_WT_I4Z_S32) */
 } qh_mat_desc;
 
 /* The last error of the calling thread ("" if none). */
