@@ -106,8 +106,8 @@ int qh_quant_to_bf16(const qh_quant* q, uint16_t* out);
 /* row_order (core.rs:108-114): packed row i <- original row out[i]. silu: gate/up interleaved per 16 rows. */
 int qh_row_order(size_t rows, int silu, size_t* out);
 
-/* Byte sizes of the gfx950 tile layout for a matrix of `rows` packed rows (a multiple of 16) and `cols` columns (of 128).
- * The codes of one matrix must fit in 4 GiB (the kernels use 32-bit offsets): QH_EINVAL beyond. */
+/* Byte sizes of the gfx950 tile layout for a matrix of `rows` packed rows (a multiple of 16) and `cols` columns (a
+ * multiple of 128). The codes of one matrix must fit in 4 GiB (the kernels use 32-bit offsets): QH_EINVAL beyond. */
 int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_bytes, size_t* scale_bytes, size_t* zero_bytes);
 
 /* The load-time repacker: rows `order[0..n)` of `q` (a Quant of bits 4 or 8, group a multiple of 128 or a whole row)
