@@ -173,3 +173,17 @@ def test_prefill_rejects_x_past_32bit_offsets(gemm):
     with pytest.raises(QhError) as e:
         gemm.run(None, 17, mat, x, y, Epi.Plain, ldx=1 << 27)
     assert "4 GiB" in str(e.value)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (80, 640), (272, 1152)])
+def test_small_and_odd_shapes(gemm, kind, n, k):
+    """Edge shapes at both kernels' boundaries: a single tile and a single group; tile counts that leave a wave's or a
+    prefill workgroup's last tiles past the matrix (3, 5 and 17 tiles); group counts that are not a multiple of 4
+    (one group per decode wave); token counts on both sides of the skinny/prefill switch and a 130-token step."""
+    for m in (1, 3, 16, 17, 130):
+        print(f"odd shape {kind} {n}x{k} m={m}", flush=True)
+        q = make_quant(170 + m, kind, n, k)
+        x = activations(171 + m, "x", m, k, outliers=0.01)
+        mat = Mat.stack(gemm, [q])
+        _check(_plain(gemm, mat, x, m), q, x, m)
