@@ -430,7 +430,8 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: the products run on one MI355X; --gpus must be 1 "
-                                   "(how they would shard is described in DESIGN.md)"}))
+                                   "(across GPUs a product would shard by output rows, or by K with its split-K "
+                                   "partials summed by an all-reduce)"}))
         sys.exit(2)
 
     import torch
