@@ -410,7 +410,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant,consumers (the last only when named)")
+    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant,consumers")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -440,7 +440,7 @@ def main():
 
     torch.cuda.init()
     gemm = Gemm.load(0)
-    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8", "dense", "dequant"}
+    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8", "dense", "dequant", "consumers"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
