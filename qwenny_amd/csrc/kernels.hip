@@ -1,9 +1,10 @@
-// The quantized-weight matrix products on gfx950 (MI355X): y = W . x for bf16 activations x [m][K] and int4 / int8
-// weights W [rows][K] in the tile layout of layout.h, f32 accumulation, on v_mfma_f32_16x16x32_bf16.
+// The quantized-weight matrix products on gfx950 (MI355X): y = W . x for bf16 activations x [m][K] and int4 / int8 /
+// dense bf16 weights W [rows][K] in the tile layout of layout.h, f32 accumulation.
 //
-// Both kernels compute D = X . W^T with the activations as the MFMA A operand (16 tokens x 32 k) and the weights as
-// the B operand (32 k x 16 outputs), so the packed tile block is the B operand as loaded. Lane l of a wave holds
-// D[token 4 (l / 16) + r][output l % 16], r = 0..3.
+// Both kernels compute D = X . W^T with the activations as the MFMA A operand and the weights as the B operand, so the
+// packed tile block is the B operand as loaded. The skinny kernel runs v_mfma_f32_16x16x32_bf16 (A 16 tokens x 32 k,
+// B 32 k x 16 outputs; lane l of a wave holds D[token 4 (l / 16) + r][output l % 16], r = 0..3), the prefill kernel
+// v_mfma_f32_32x32x16_bf16 (its layout below).
 //
 // skinny_kernel (m <= 16, decode and MTP verify): HBM-bound. The weights are streamed once with 16-byte loads (a wave
 // reads each (tile, group) block as one contiguous KiB) and turned into bf16 (128 + q) with one and-or per two values;
@@ -12,10 +13,12 @@
 // by the wave's tiles). K is split over the waves of a workgroup (reduced through LDS) and, for plain products, over
 // the grid (the split-K partials of the output contract).
 //
-// prefill_kernel (m > 16): MFMA-bound. A workgroup of 8 waves computes up to 256 tokens x 256 outputs; the
-// activation tile goes global -> LDS directly (global_load_lds) into double-buffered, XOR-swizzled 64-column stages,
-// each wave dequantizes its own outputs' weights straight from global memory into bf16 registers ((q - z) s in f32,
-// rounded once), and the workgroups are mapped XCD-aware so that those sharing a weight tile run on one XCD's L2.
+// prefill_kernel (m > 16): MFMA-bound. A workgroup computes up to 256 tokens x 256 outputs (8 waves of 256 x 32, or
+// 256 x 192 on 12 waves of 128 x 32, or smaller tiles for short steps); the activation tile goes global -> LDS directly
+// (global_load_lds) into double-buffered, XOR-swizzled 64-column stages, each wave dequantizes its own outputs'
+// weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), the workgroups are mapped
+// XCD-aware (an XCD's workgroups share a token tile's activations in its L2), and a badly filled last round is spread
+// over the resident workgroups by groups of K (stream-K).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
