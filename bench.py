@@ -313,6 +313,28 @@ def dequant_line(args):
     return {"dequant_i4_to_bf16_GBps": gbs}
 
 
+SET_4B = [(2560, 4096), (4096, 2560), (2560, 1024), (2560, 9728), (2560, 9728), (9728, 2560)]
+
+
+def set4b_line(gemm, args):
+    """the 4B-scale layer set, int4 with packed zero points, at M = 1 and 8, 12 distinct
+    device copies (590 MB per pass, beyond the 256 MB MALL), HIP graphs: HBM GB/s over the algorithmic bytes."""
+    from qwenny_amd import Epi
+
+    mats = [upload_copies(gemm, quant(600 + i, "i4z", k, n), 12) for i, (k, n) in enumerate(SET_4B)]
+    out = {}
+    for m in (1, 8):
+        st = Step(gemm, m, 9728)
+        for c in range(12):
+            for ms_, (k, n) in zip(mats, SET_4B):
+                st.add(ms_[c], Epi.Plain, int4_bytes(k, n, m, zp=True), 2 * m * k * n)
+        ms = time_step(st, args.steps, args.warmup, not args.no_graph)
+        out[f"m{m}_GBps"] = round(st.bytes() / (ms * 1e-3) / 1e9, 1)
+        print(f"# 4B set with zero points M={m}: {ms * 1e3 / len(st.launches):.2f} us per launch, "
+              f"{out[f'm{m}_GBps']} GB/s", file=sys.stderr, flush=True)
+    return {"set4b_i4z": out}
+
+
 def consumers_line(args):
     """The partials consumers and the LoRA epilogue at 27B sizes, after the down projection (K 17408 -> 5120 rows) and
     on [gate; up] (34816 rows, rank 16): M = 1 (34 split-K partials) and M = 2048 (one). HBM GB/s over the bytes each
@@ -410,7 +432,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant,consumers")
+    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant,set4b,consumers")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -440,7 +462,7 @@ def main():
 
     torch.cuda.init()
     gemm = Gemm.load(0)
-    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8", "dense", "dequant", "consumers"}
+    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8", "dense", "dequant", "set4b", "consumers"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
@@ -538,6 +560,8 @@ def main():
         extra.update(dense_lines(gemm, args))
     if "dequant" in only:
         extra.update(dequant_line(args))
+    if "set4b" in only:
+        extra.update(set4b_line(gemm, args))
     if "consumers" in only:
         extra.update(consumers_line(args))
 
