@@ -80,7 +80,7 @@ class Step:
         from qwenny_amd import Epi
 
         rows = mat.rows
-        split = mat.split(self.m) if epi == Epi.Plain and self.m <= 16 else 1
+        split = mat.split(self.m) if epi == Epi.Plain else 1
         key = (rows, split, epi)
         if key not in self.ys:
             self.ys[key] = torch.empty(split * self.m * rows, dtype=torch.float32, device="cuda")

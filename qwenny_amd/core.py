@@ -18,6 +18,12 @@ from ._lib import MatDesc, QuantC, check, lib
 P = ctypes.c_void_p
 
 
+# Token counts the decode (skinny) kernel takes: its products are exact (every weight bf16 (128 + q) times x summed in
+# f32, the scale after), and plain ones return split-K partials; above it the prefill kernel rounds each dequantized
+# weight to bf16 once and plain products return one partial (csrc/kernels.h SKINNY_MAX_M).
+SKINNY_MAX_M = 48
+
+
 class Wt(IntEnum):
     """How a matrix is stored (src/cuda/core.rs:65-79). I4 replaces Wt::Marlin, I4Z Wt::MarlinZ; the _S32 forms keep
     f32 scales (scales bf16 does not hold exactly)."""

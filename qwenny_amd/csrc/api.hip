@@ -277,16 +277,18 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
     const int ng = !is_bf16(m->wt) && G % 4 == 0 && !few ? 4 : 1;
     const int want_wt = ctx->skinny_tile_waves > 0 ? ctx->skinny_tile_waves : (tokens <= 2 ? 4 : 8);
     if (plain) {
-        const int wt = std::max(1, std::min(want_wt, cols));
+        const int wt = std::max(1, std::min({want_wt, cols, tokens > 16 ? 8 : 16}));
         return Partition{wt, wt, G / ng, ng};
     }
     const size_t per_group = std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's activations
-    const int wt = std::max(1, std::min({tokens <= 2 ? 2 : 8, cols, ctx->skinny_max_w}));
+    // above 16 tokens (several 16-token blocks per wave) workgroups of at most 8 waves: the kernel's register budget
+    const int max_w = tokens > 16 ? std::min(ctx->skinny_max_w, 8) : ctx->skinny_max_w;
+    const int wt = std::max(1, std::min({tokens <= 2 ? 2 : 8, cols, max_w}));
     const long wgs = (cols + wt - 1) / wt;
     // wave rows: dividing the chunks of K, within the wave and LDS limits; the fewest that make a workgroup of at least
     // 4 waves, more only while the launch has fewer than skinny_fill waves per CU (measured: extra rows add LDS
     // reductions and lose occupancy; fewer than 4 waves walk K in too many barrier-separated super-chunks)
-    const int nchunks = G / ng, wmax = std::min(ctx->skinny_max_w / wt, nchunks);
+    const int nchunks = G / ng, wmax = std::min(max_w / wt, nchunks);
     int wk = 1;
     for (int w = 1; w <= wmax; w++) {
         if (nchunks % w || (size_t)w * ng * per_group > SKINNY_X_LDS) continue;

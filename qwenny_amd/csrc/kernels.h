@@ -63,7 +63,7 @@ constexpr int PF_SK_ITEMS_MAX = 4096;
 constexpr int PF_SK_FIXUP = 12;
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
-constexpr int SKINNY_MAX_M = 16;
+constexpr int SKINNY_MAX_M = 48;  // the skinny kernel up to 48 tokens (three 16-token blocks per MFMA pass)
 // 16-row tiles per wave in the skinny kernel, and its pipeline depth (groups whose loads are in flight + 1).
 #ifndef QH_SKINNY_TILES
 #define QH_SKINNY_TILES 2

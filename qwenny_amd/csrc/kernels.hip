@@ -6,14 +6,14 @@
 // B 32 k x 16 outputs; lane l of a wave holds D[token 4 (l / 16) + r][output l % 16], r = 0..3), the prefill kernel
 // v_mfma_f32_32x32x16_bf16 (its layout below).
 //
-// skinny_kernel (m <= 16, decode and MTP verify): HBM-bound. The weights are streamed once with 16-byte loads (a wave
+// skinny_kernel (m <= 48, decode, MTP verify and small batches): HBM-bound. The weights are streamed once with 16-byte loads (a wave
 // reads each (tile, group) block as one contiguous KiB) and turned into bf16 (128 + q) with one and-or per two values;
 // the MFMA sums x (128 + q) exactly in f32 per 128-column group, and the group's scale and zero point are applied
 // after it: acc += s (D - (128 + z) sum_k x), where sum_k x comes from one more MFMA against ones per k32 step (shared
 // by the wave's tiles). K is split over the waves of a workgroup (reduced through LDS) and, for plain products, over
 // the grid (the split-K partials of the output contract).
 //
-// prefill_kernel (m > 16): MFMA-bound. A workgroup computes up to 256 tokens x 256 outputs (8 waves of 256 x 32, or
+// prefill_kernel (m > 48): MFMA-bound. A workgroup computes up to 256 tokens x 256 outputs (8 waves of 256 x 32, or
 // 256 x 192 on 12 waves of 128 x 32, or smaller tiles for short steps); the activation tile goes global -> LDS directly
 // (global_load_lds) into double-buffered, XOR-swizzled 64-column stages, each wave dequantizes its own outputs'
 // weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), the workgroups are mapped
@@ -181,11 +181,9 @@ __device__ __forceinline__ int zero_of(const uint16_t* zeros, int tile, int G, i
 // (every wave of it reads them with ds_read_b128 instead of fetching them from L2). The grid's y dimension splits the
 // super-chunks of K (plain products: split-K partials); WK waves' partial sums are reduced through LDS.
 
-// activation pieces (16 bytes) each thread loads ahead of the weights
-constexpr int XPT = 1;
 
-template <int F, int EPI, int NR, int T, int NG>
-__global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
+template <int F, int EPI, int NR, int T, int NG, int TB>
+__global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int CW = CodeWords<F>::N;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -202,18 +200,24 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
     int tt[T];
 #pragma unroll
     for (int t = 0; t < T; t++) tt[t] = min(tile0 + t, tiles - 1);
-    const int xtok = min(l16, M - 1);  // lanes of tokens past M read row M - 1: their results are never stored
+    // token block b (16 tokens): lanes read activation row 16 b + l16 (rows past M read row M - 1: their results are
+    // never stored)
+    int xtok[TB];
+#pragma unroll
+    for (int b = 0; b < TB; b++) xtok[b] = min(16 * b + l16, M - 1);
 
     const uint32_t magic_s = a.bf16_magic, mask = a.nib_mask;
     uint32_t magic;  // in a VGPR (copied once; only VALU reads it) so that each pair is one v_and_or_b32
     asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(magic_s));
     const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
-    float acc[T][NR];
+    float acc[TB][T][NR];
 #pragma unroll
-    for (int t = 0; t < T; t++)
+    for (int b = 0; b < TB; b++)
 #pragma unroll
-        for (int r = 0; r < NR; r++) acc[t][r] = 0.0f;
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) acc[b][t][r] = 0.0f;
 
     for (int c = c0; c < c1; c++) {
         const int gs = c * CH;              // first group of the super-chunk
@@ -223,6 +227,7 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
         //    the rest, if any, afterwards
         const int rowc = CH * 16;  // 16-byte pieces per row
         const int npieces = M * rowc;
+        constexpr int XPT = TB;  // activation pieces each thread loads ahead of the weights
         u32x4 xv[XPT];
         int xo[XPT];
 #pragma unroll
@@ -273,39 +278,37 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
             *(u32x4*)(xs_lds + (size_t)tok * xpitch + 8 * pc) = *(const u32x4*)src;
         }
         __syncthreads();
-        // 3. compute the wave's groups
+        // 3. compute the wave's groups: each tile's B fragments once, against every token block
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
-            const __bf16* xrow = xs_lds + (size_t)xtok * xpitch + (wk * NG + gi) * QG + 8 * kq;
-            u32x4 xa[4];
+            u32x4 xa[TB][4];
+            f32x4 xsum[TB];
 #pragma unroll
-            for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow + 32 * j);
-            f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int b = 0; b < TB; b++) {
+                const __bf16* xrow = xs_lds + (size_t)xtok[b] * xpitch + (wk * NG + gi) * QG + 8 * kq;
 #pragma unroll
-            for (int j = 0; j < 4 && !(F & F_BF16); j++) xsum = mfma(xa[j], ones, xsum);
+                for (int j = 0; j < 4; j++) xa[b][j] = *(const u32x4*)(xrow + 32 * j);
+                xsum[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4 && !(F & F_BF16); j++) xsum[b] = mfma(xa[b][j], ones, xsum[b]);
+            }
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+                bf16x8 bw[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    bf16x8 b;
                     if (F & F_BF16)
-                        b = __builtin_bit_cast(bf16x8, code[gi][t][j]);
+                        bw[j] = __builtin_bit_cast(bf16x8, code[gi][t][j]);
                     else if (F & F_I8)
-                        b = i8_biased(code[gi][t][j >> 1][2 * (j & 1)], code[gi][t][j >> 1][2 * (j & 1) + 1]);
+                        bw[j] = i8_biased(code[gi][t][j >> 1][2 * (j & 1)], code[gi][t][j >> 1][2 * (j & 1) + 1]);
                     else
-                        b = i4_biased(code[gi][t][0][j], mask, magic);
-                    d = mfma(xa[j], b, d);
-                }
-                if (F & F_BF16) {  // the weights themselves: no scale, no zero point
-#pragma unroll
-                    for (int r = 0; r < NR; r++) acc[t][r] += d[r];
-                    continue;
+                        bw[j] = i4_biased(code[gi][t][0][j], mask, magic);
                 }
                 const int g = gw + gi;
                 // the group's scale from the raw scale words: f32 one per word; bf16 two per word (NG == 4) or one
-                float sc;
-                if (F & F_S32) {
+                float sc = 1.0f, cz = 0.0f;
+                if (F & F_BF16) {
+                } else if (F & F_S32) {
                     sc = __uint_as_float(sraw[t][NG == 4 ? gi : 0]);
                 } else if (NG == 4) {
                     const uint32_t w = sraw[t][gi >> 1];
@@ -313,10 +316,22 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
                 } else {
                     sc = __uint_as_float(sraw[t][0] << 16);
                 }
-                const float cz = (F & F_ZP) ? (float)(128 + (int)((zraw[t] >> (4 * (g & 3))) & 15u))
-                                            : ((F & F_I8) ? 128.0f : 136.0f);  // 128 + zero point
+                if (!(F & F_BF16))
+                    cz = (F & F_ZP) ? (float)(128 + (int)((zraw[t] >> (4 * (g & 3))) & 15u))
+                                    : ((F & F_I8) ? 128.0f : 136.0f);  // 128 + zero point
 #pragma unroll
-                for (int r = 0; r < NR; r++) acc[t][r] += sc * (d[r] - cz * xsum[r]);
+                for (int b = 0; b < TB; b++) {
+                    f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) d = mfma(xa[b][j], bw[j], d);
+                    if (F & F_BF16) {  // the weights themselves: no scale, no zero point
+#pragma unroll
+                        for (int r = 0; r < NR; r++) acc[b][t][r] += d[r];
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < NR; r++) acc[b][t][r] += sc * (d[r] - cz * xsum[b][r]);
+                    }
+                }
             }
         }
     }
@@ -326,25 +341,32 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
     if (WK > 1) {
         if (wk > 0) {
 #pragma unroll
-            for (int t = 0; t < T; t++)
+            for (int b = 0; b < TB; b++)
 #pragma unroll
-                for (int r = 0; r < NR; r++) red[((((wk - 1) * WT + wt) * T + t) * NR + r) * 64 + lane] = acc[t][r];
+                for (int t = 0; t < T; t++)
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+                        red[(((((wk - 1) * WT + wt) * TB + b) * T + t) * NR + r) * 64 + lane] = acc[b][t][r];
         }
         __syncthreads();
         lead = wk == 0;
         if (lead)
             for (int w = 1; w < WK; w++)
 #pragma unroll
-                for (int t = 0; t < T; t++)
+                for (int b = 0; b < TB; b++)
 #pragma unroll
-                    for (int r = 0; r < NR; r++)
-                        acc[t][r] += red[((((w - 1) * WT + wt) * T + t) * NR + r) * 64 + lane];
+                    for (int t = 0; t < T; t++)
+#pragma unroll
+                        for (int r = 0; r < NR; r++)
+                            acc[b][t][r] += red[(((((w - 1) * WT + wt) * TB + b) * T + t) * NR + r) * 64 + lane];
     }
 
     const int sp = blockIdx.y;
-    unsigned long long key[NR];
+    unsigned long long key[TB][NR];
 #pragma unroll
-    for (int r = 0; r < NR; r++) key[r] = 0;
+    for (int b = 0; b < TB; b++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) key[b][r] = 0;
     if (lead) {
 #pragma unroll
         for (int t = 0; t < T; t++) {
@@ -352,27 +374,32 @@ __global__ __launch_bounds__(1024) void skinny_kernel(Launch a) {
             if (tile >= tiles) break;
             const int out = tile * TILE + l16;
 #pragma unroll
-            for (int r = 0; r < NR; r++) {
-                const int tok = 4 * kq + r;
-                const float v = acc[t][r];
-                if (EPI == EPI_SILU) {
-                    const float up = __shfl_xor(v, 8);
-                    if (l16 < 8 && tok < M)
-                        ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(v) * up);
-                } else {
-                    if (tok < M) ((float*)a.y)[((size_t)sp * M + tok) * a.ldy + out] = v;
-                    if (EPI == EPI_ARGMAX && tok < M && out < a.valid) key[r] = max_u64(key[r], argmax_key(v, out));
+            for (int b = 0; b < TB; b++)
+#pragma unroll
+                for (int r = 0; r < NR; r++) {
+                    const int tok = 16 * b + 4 * kq + r;
+                    const float v = acc[b][t][r];
+                    if (EPI == EPI_SILU) {
+                        const float up = __shfl_xor(v, 8);
+                        if (l16 < 8 && tok < M)
+                            ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(v) * up);
+                    } else {
+                        if (tok < M) ((float*)a.y)[((size_t)sp * M + tok) * a.ldy + out] = v;
+                        if (EPI == EPI_ARGMAX && tok < M && out < a.valid)
+                            key[b][r] = max_u64(key[b][r], argmax_key(v, out));
+                    }
                 }
-            }
         }
     }
     if (EPI == EPI_ARGMAX) {
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const unsigned long long k = group16_max(key[r]);
-            const int tok = 4 * kq + r;
-            if (lead && l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
-        }
+        for (int b = 0; b < TB; b++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const unsigned long long k = group16_max(key[b][r]);
+                const int tok = 16 * b + 4 * kq + r;
+                if (lead && l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
+            }
         argmax_finish(a);
     }
 }
@@ -740,26 +767,29 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
 // ---------------------------------------------------------------------------------------------------------------
 // launchers
 
-template <int F, int EPI, int NR, int NG>
+template <int F, int EPI, int NR, int NG, int TB>
 static hipError_t skinny_ng(const Launch& l) {
     const int tiles = l.rows / TILE;
     const int per_wg = SKINNY_TILES * l.tile_waves;
     dim3 grid((tiles + per_wg - 1) / per_wg, l.split);
-    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG>), grid, dim3(64 * l.waves), skinny_lds(l),
+    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.waves), skinny_lds(l),
                        l.stream, l);
     return hipGetLastError();
 }
 
-template <int F, int EPI, int NR>
+template <int F, int EPI, int NR, int TB = 1>
 static hipError_t skinny_nr(const Launch& l) {
     if constexpr ((F & F_BF16) != 0)
-        return skinny_ng<F, EPI, NR, 1>(l);  // one 4 KiB group of a tile per wave
+        return skinny_ng<F, EPI, NR, 1, TB>(l);  // one 4 KiB group of a tile per wave
     else
-        return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4>(l) : skinny_ng<F, EPI, NR, 1>(l);
+        return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4, TB>(l) : skinny_ng<F, EPI, NR, 1, TB>(l);
 }
 
+// token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
+    if (l.m > 32) return skinny_nr<F, EPI, 4, 3>(l);
+    if (l.m > 16) return skinny_nr<F, EPI, 4, 2>(l);
     switch (l.m) {
         case 1: return skinny_nr<F, EPI, 1>(l);
         case 2: return skinny_nr<F, EPI, 2>(l);
@@ -874,9 +904,9 @@ template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(const Launch& l);
 
 #ifdef QH_PART_DISPATCH
 size_t skinny_lds(const Launch& l) {
-    const int wk = l.waves / l.tile_waves;
+    const int wk = l.waves / l.tile_waves, tb = (l.m + 15) / 16;
     const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
-    return x + (size_t)(wk - 1) * l.tile_waves * SKINNY_TILES * 4 * 64 * sizeof(float);
+    return x + (size_t)(wk - 1) * l.tile_waves * tb * SKINNY_TILES * 4 * 64 * sizeof(float);
 }
 
 template <int F>

@@ -28,7 +28,7 @@ def _weights(seed, rows, cols):
 def _plain(gemm, mat, x, m):
     import torch
 
-    split = mat.split(m) if m <= 16 else 1
+    split = mat.split(m)
     y = torch.full((split, m, mat.rows), float("nan"), dtype=torch.float32, device="cuda")
     assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == split
     torch.cuda.synchronize()

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle
-from qwenny_amd import Epi, Mat, Wt, row_order
+from qwenny_amd import SKINNY_MAX_M, Epi, Mat, Wt, row_order
 from qwenny_amd.synth import activations, bf16_to_f32
 from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, sub_quant,
                            to_dev)
@@ -25,7 +25,7 @@ WT_OF = {"i4": Wt.I4, "i4z": Wt.I4Z, "i8": Wt.I8}
 def _plain(gemm, mat, x, m, stream=None):
     import torch
 
-    split = mat.split(m) if m <= 16 else 1
+    split = mat.split(m)
     y = torch.full((split, m, mat.rows), float("nan"), dtype=torch.float32, device="cuda")
     got = gemm.run(stream, m, mat, to_dev(x), y, Epi.Plain)
     torch.cuda.synchronize()
@@ -38,7 +38,7 @@ def _check(got, q, x, m):
     want = oracle_y(q, x)
     err = rel_err(got, want)
     assert err <= TOL, f"max|err|/rms {err:.3e} vs the oracle"
-    exact = want if m <= 16 else emulate_bf16_weights(q, x)
+    exact = want if m <= SKINNY_MAX_M else emulate_bf16_weights(q, x)
     err = rel_err(got, exact)
     assert err <= 1e-4, f"max|err|/rms {err:.3e} vs the kernel's arithmetic"
 
@@ -55,7 +55,7 @@ def test_skinny_plain(gemm, kind, m):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("m", [17, 64, 130, 256, 300])
+@pytest.mark.parametrize("m", [17, 33, 48, 49, 64, 130, 256, 300])
 def test_prefill_plain(gemm, kind, m):
     print(f"prefill plain {kind} m={m}", flush=True)
     q = make_quant(21 + m, kind, 384, 768)
@@ -83,7 +83,7 @@ def test_silu(gemm, kind, m):
     assert gemm.run(None, m, mat, to_dev(x), y, Epi.Silu) == 1
     torch.cuda.synchronize()
     got = y.float().cpu().numpy()
-    if m <= 16:
+    if m <= SKINNY_MAX_M:
         full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1)
         tol = TOL
     else:
@@ -161,17 +161,20 @@ def test_argmax_rejects_too_many_rows(gemm):
 
 
 def test_prefill_rejects_x_past_32bit_offsets(gemm):
-    """Above 16 tokens the kernels address x's rows with 32-bit byte offsets: a row stride that puts token 16 at 4 GiB
-    is refused before any launch."""
+    """Above SKINNY_MAX_M tokens the prefill kernel addresses x's rows with 32-bit byte offsets: a row stride that
+    puts the last token past 4 GiB is refused before any launch."""
     import torch
 
     from qwenny_amd._lib import QhError
 
+    m = SKINNY_MAX_M + 1
     mat = Mat.stack(gemm, [make_quant(45, "i4", 64, 128)])
-    x = torch.zeros((17, 128), dtype=torch.bfloat16, device="cuda")
-    y = torch.zeros((17, 64), dtype=torch.float32, device="cuda")
+    x = torch.zeros((m, 128), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((m, 64), dtype=torch.float32, device="cuda")
+    ldx = 1 << 26  # (m - 1) * ldx * 2 bytes = 6 GiB
+    assert (m - 1) * ldx * 2 > 1 << 32
     with pytest.raises(QhError) as e:
-        gemm.run(None, 17, mat, x, y, Epi.Plain, ldx=1 << 27)
+        gemm.run(None, m, mat, x, y, Epi.Plain, ldx=ldx)
     assert "4 GiB" in str(e.value)
 
 
@@ -181,7 +184,7 @@ def test_small_and_odd_shapes(gemm, kind, n, k):
     """Edge shapes at both kernels' boundaries: a single tile and a single group; tile counts that leave a wave's or a
     prefill workgroup's last tiles past the matrix (3, 5 and 17 tiles); group counts that are not a multiple of 4
     (one group per decode wave); token counts on both sides of the skinny/prefill switch and a 130-token step."""
-    for m in (1, 3, 16, 17, 130):
+    for m in (1, 3, 16, 17, 48, 49, 130):
         print(f"odd shape {kind} {n}x{k} m={m}", flush=True)
         q = make_quant(170 + m, kind, n, k)
         x = activations(171 + m, "x", m, k, outliers=0.01)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from qwenny_amd import Epi, Mat, Quant, Wt, synth
+from qwenny_amd import SKINNY_MAX_M, Epi, Mat, Quant, Wt, synth
 from qwenny_amd.checkpoint import Checkpoint, save_safetensors
 from qwenny_amd.synth import activations
 from tests.helpers import TOL, make_quant, oracle_y, rel_err, sub_quant, to_dev
@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 def _plain(gemm, mat, x, m, whole=False, ldx=0, xdev=None):
     import torch
 
-    split = 1 if whole or m > 16 else mat.split(m)
+    split = 1 if whole else mat.split(m)
     y = torch.full((split, m, mat.rows), float("nan"), dtype=torch.float32, device="cuda")
     got = gemm.run_split(None, m, mat, to_dev(x) if xdev is None else xdev, y, Epi.Plain, whole, ldx=ldx)
     torch.cuda.synchronize()
@@ -53,7 +53,7 @@ def test_marlin_rows_then_put_block(gemm, kind, m):
     assert (mat.rows, mat.valid, mat.wt) == (128, 32, Wt.I4Z if kind == "i4z" else Wt.I4)
     x = activations(9 + m, "x", m, k)
     got = _plain(gemm, mat, x, m)
-    tol = 1e-4 if m <= 16 else TOL
+    tol = 1e-4 if m <= SKINNY_MAX_M else TOL
     assert rel_err(got[:, :32], oracle_y(sub_quant(q, first), x)) <= tol
     logits, keys = _argmax(gemm, mat, x)
     assert (keys == oracle.argmax_keys(logits, 32)).all()
@@ -98,7 +98,7 @@ def test_wide_groups(gemm, group, m):
     assert q.group == group
     x = activations(11, "x", m, 1024)
     got = _plain(gemm, Mat.stack(gemm, [q]), x, m)
-    assert rel_err(got, oracle_y(q, x)) <= (1e-4 if m <= 16 else TOL)
+    assert rel_err(got, oracle_y(q, x)) <= (1e-4 if m <= SKINNY_MAX_M else TOL)
 
 
 @pytest.mark.parametrize("zp", [False, True])
@@ -114,7 +114,7 @@ def test_f32_scales(gemm, zp, m):
     mat = Mat.stack(gemm, [q2])
     assert mat.wt == (Wt.I4Z_S32 if zp else Wt.I4_S32)
     x = activations(12, "x", m, 512)
-    assert rel_err(_plain(gemm, mat, x, m), oracle_y(q2, x)) <= (1e-4 if m <= 16 else TOL)
+    assert rel_err(_plain(gemm, mat, x, m), oracle_y(q2, x)) <= (1e-4 if m <= SKINNY_MAX_M else TOL)
 
 
 @pytest.mark.parametrize("m", [1, 4, 33])
@@ -128,7 +128,7 @@ def test_strided_activations(gemm, m):
     x = wide[:, :k]
     xdev = torch.from_numpy(np.ascontiguousarray(wide).view(np.int16)).cuda().view(torch.bfloat16)
     got = _plain(gemm, Mat.stack(gemm, [q]), x, m, ldx=ldx, xdev=xdev)
-    assert rel_err(got, oracle_y(q, np.ascontiguousarray(x))) <= (1e-4 if m <= 16 else TOL)
+    assert rel_err(got, oracle_y(q, np.ascontiguousarray(x))) <= (1e-4 if m <= SKINNY_MAX_M else TOL)
 
 
 @pytest.mark.parametrize("kind", ["i4", "i8"])
@@ -145,8 +145,10 @@ def test_whole(gemm, kind, m):
 
 def test_part_len(gemm):
     mats = [Mat.stack(gemm, [make_quant(78, "i4", 256, k)]) for k in (512, 4096)]
-    need = max(m.split(n) * n * m.rows for m in mats for n in range(1, 17))
-    assert gemm.part_len(mats, 16) >= need
+    for max_tok in (16, SKINNY_MAX_M, SKINNY_MAX_M + 1, 300):
+        need = max(m.split(n) * n * m.rows for m in mats for n in range(1, max_tok + 1))
+        assert gemm.part_len(mats, max_tok) >= need, max_tok
+    assert mats[1].split(SKINNY_MAX_M) > 1 and mats[1].split(SKINNY_MAX_M + 1) == 1
 
 
 def test_checkpoint_end_to_end(gemm, tmp_path):

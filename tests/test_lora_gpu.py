@@ -5,14 +5,14 @@ an unmerged adapter's delta s_t B (A x) added to a plain product's split 0 (lora
 Against the oracle on random partials and B (f32 sums, f32 dot products in column order: 1e-5 of the output's RMS),
 and end to end: the product's partials from an int4 matrix, xa from the stacked A product (a dense bf16 matrix),
 lora_add, then sum_parts, against W x + s B (A x) in f64 (1e-4 of RMS, the int4 weights rounded to bf16 as the prefill
-kernel does above 16 tokens); lora_silu against silu(g + dg) (u + du) with the bf16 rounding of the output.
+kernel does above 48 tokens); lora_silu against silu(g + dg) (u + du) with the bf16 rounding of the output.
 """
 
 import numpy as np
 import pytest
 
 import oracle
-from qwenny_amd import Epi, Mat, lora_add, lora_silu, row_order, sum_parts
+from qwenny_amd import SKINNY_MAX_M, Epi, Mat, lora_add, lora_silu, row_order, sum_parts
 from qwenny_amd.synth import activations, bf16_to_f32, f32_to_bf16
 from tests.helpers import bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, to_dev
 
@@ -77,10 +77,10 @@ def test_lora_add_end_to_end(gemm, m):
     tok_slot = (np.arange(m) % 2).astype(np.int32)
     x = activations(152, "x", m, k)
     xd = to_dev(x)
-    split = w.split(m) if m <= 16 else 1
+    split = w.split(m)
     y = torch.empty((split, m, n_out), dtype=torch.float32, device="cuda")
     assert gemm.run(None, m, w, xd, y, Epi.Plain) == split
-    split_a = amat.split(m) if m <= 16 else 1
+    split_a = amat.split(m)
     xa = torch.empty((split_a, m, 2 * rank), dtype=torch.float32, device="cuda")
     assert gemm.run(None, m, amat, xd, xa, Epi.Plain) == split_a
     lora_add(None, xa, split_a, 2 * rank, _b16(b), rank, n_out, _dev(tab), _dev(tok_slot), _dev(slot_scale), m, y[0])
@@ -92,7 +92,7 @@ def test_lora_add_end_to_end(gemm, m):
     bf = b.astype(np.float64)
     delta = np.concatenate([xs[:, :rank] @ bf[:512].T, xs[:, rank:] @ bf[512:].T], axis=1)
     # decode products are exact; prefill ones round each int4 weight to bf16 once (the same bar on that arithmetic)
-    base = oracle_y(q, x) if m <= 16 else emulate_bf16_weights(q, x)
+    base = oracle_y(q, x) if m <= SKINNY_MAX_M else emulate_bf16_weights(q, x)
     want = base + slot_scale[tok_slot][:, None] * delta
     assert rel_err(out.cpu().numpy(), want) <= 1e-4
 
