@@ -294,21 +294,41 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
             }
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                bf16x8 bw[4];
+                // B fragment j of tile t (one token block dequantizes it next to its MFMA, fewer live registers;
+                // several keep all four for their blocks)
+                auto frag = [&](int j) -> bf16x8 {
+                    if (F & F_BF16) return __builtin_bit_cast(bf16x8, code[gi][t][j]);
+                    if (F & F_I8)
+                        return i8_biased(code[gi][t][j >> 1][2 * (j & 1)], code[gi][t][j >> 1][2 * (j & 1) + 1]);
+                    return i4_biased(code[gi][t][0][j], mask, magic);
+                };
+                f32x4 d[TB];
+                if constexpr (TB == 1) {
+                    d[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    if (F & F_BF16)
-                        bw[j] = __builtin_bit_cast(bf16x8, code[gi][t][j]);
-                    else if (F & F_I8)
-                        bw[j] = i8_biased(code[gi][t][j >> 1][2 * (j & 1)], code[gi][t][j >> 1][2 * (j & 1) + 1]);
-                    else
-                        bw[j] = i4_biased(code[gi][t][0][j], mask, magic);
+                    for (int j = 0; j < 4; j++) d[0] = mfma(xa[0][j], frag(j), d[0]);
+                } else {
+                    bf16x8 bw[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) bw[j] = frag(j);
+#pragma unroll
+                    for (int b = 0; b < TB; b++) {
+                        d[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int j = 0; j < 4; j++) d[b] = mfma(xa[b][j], bw[j], d[b]);
+                    }
+                }
+                if (F & F_BF16) {  // the weights themselves: no scale, no zero point
+#pragma unroll
+                    for (int b = 0; b < TB; b++)
+#pragma unroll
+                        for (int r = 0; r < NR; r++) acc[b][t][r] += d[b][r];
+                    continue;
                 }
                 const int g = gw + gi;
                 // the group's scale from the raw scale words: f32 one per word; bf16 two per word (NG == 4) or one
-                float sc = 1.0f, cz = 0.0f;
-                if (F & F_BF16) {
-                } else if (F & F_S32) {
+                float sc;
+                if (F & F_S32) {
                     sc = __uint_as_float(sraw[t][NG == 4 ? gi : 0]);
                 } else if (NG == 4) {
                     const uint32_t w = sraw[t][gi >> 1];
@@ -316,22 +336,12 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
                 } else {
                     sc = __uint_as_float(sraw[t][0] << 16);
                 }
-                if (!(F & F_BF16))
-                    cz = (F & F_ZP) ? (float)(128 + (int)((zraw[t] >> (4 * (g & 3))) & 15u))
-                                    : ((F & F_I8) ? 128.0f : 136.0f);  // 128 + zero point
+                const float cz = (F & F_ZP) ? (float)(128 + (int)((zraw[t] >> (4 * (g & 3))) & 15u))
+                                            : ((F & F_I8) ? 128.0f : 136.0f);  // 128 + zero point
 #pragma unroll
-                for (int b = 0; b < TB; b++) {
-                    f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int b = 0; b < TB; b++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) d = mfma(xa[b][j], bw[j], d);
-                    if (F & F_BF16) {  // the weights themselves: no scale, no zero point
-#pragma unroll
-                        for (int r = 0; r < NR; r++) acc[b][t][r] += d[r];
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < NR; r++) acc[b][t][r] += sc * (d[r] - cz * xsum[b][r]);
-                    }
-                }
+                    for (int r = 0; r < NR; r++) acc[b][t][r] += sc * (d[b][r] - cz * xsum[b][r]);
             }
         }
     }
