@@ -298,40 +298,9 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
     return Partition{wt, wt * wk, 1, ng};
 }
 
-extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
-    if (!ctx || !m) return fail(QH_EINVAL, "split: null");
-    if (n == 0 || n > (size_t)SKINNY_MAX_M) return 1;
-    return skinny_partition(ctx, m, n, true).split;
-}
-
-extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok) {
-    size_t len = 0;
-    for (size_t i = 0; ctx && mats && i < count; i++) {
-        if (!mats[i]) continue;
-        size_t rows = std::max(max_tok, (size_t)qh_mat_split(ctx, mats[i], 1) * std::min(max_tok, (size_t)SKINNY_MAX_M));
-        len = std::max(len, rows * mats[i]->rows);
-    }
-    return len;
-}
-
-extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
-                       const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
-    if (!ctx || !w || !x || !y) return fail(QH_EINVAL, "gemm: null");
-    if (epi != QH_EPI_PLAIN && epi != QH_EPI_SILU && epi != QH_EPI_ARGMAX) return fail(QH_EINVAL, "epilogue %d", epi);
-    if (epi == QH_EPI_ARGMAX && !keys) return fail(QH_EINVAL, "argmax without keys");
-    if (epi == QH_EPI_SILU && w->rows % 16) return fail(QH_EINVAL, "SwiGLU of %zu rows", w->rows);
-    if (ldx == 0) ldx = w->cols;
-    if (ldx < w->cols || ldx % 8 || (uintptr_t)x % 16)
-        return fail(QH_EINVAL, "x rows of %zu elements at %p: 16-byte aligned rows of at least %zu", ldx, x, w->cols);
-    const size_t m = epi == QH_EPI_ARGMAX ? n_out : n;
-    if (m == 0) return 1;
-    if (epi == QH_EPI_ARGMAX && m > (size_t)ARGMAX_MAX_TOK)
-        return fail(QH_EINVAL, "argmax over %zu logit rows: at most %d", m, ARGMAX_MAX_TOK);
-    if (m > (1u << 24) || w->rows > (1u << 30) || ldx > (1u << 30)) return fail(QH_EINVAL, "gemm: sizes too large");
-    // the prefill kernel addresses activation rows (the n token rows, also those the argmax gathers) with 32-bit byte
-    // offsets from x
-    if (m > (size_t)SKINNY_MAX_M && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
-        return fail(QH_EINVAL, "gemm: %zu token rows of %zu elements: x must fit in 4 GiB", n, ldx);
+// The launch of a product of m tokens (epi, x, y and keys as qh_gemm takes them; `whole`: one partial).
+static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, size_t ldx, size_t m,
+                          const int32_t* out_rows, void* y, int epi, uint64_t* keys, int whole, void* stream) {
     Launch l{};
     l.codes = w->codes;
     l.scales = w->scales;
@@ -360,6 +329,8 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     l.sk_count = (unsigned*)((uint8_t*)ctx->sk_scratch + PF_SK_PART_BYTES);
     l.stream_k = ctx->stream_k;
     l.nib_mask = 0x000F000Fu;
+    l.ks = 1;
+    l.whole = whole;
     if (m <= (size_t)SKINNY_MAX_M) {
         Partition p = skinny_partition(ctx, w, m, epi == QH_EPI_PLAIN && !whole);
         l.tile_waves = p.tile_waves;
@@ -369,8 +340,54 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     } else {
         l.tile_waves = 4;
         l.waves = 4;
-        l.split = 1;
+        l.split = 1;  // the prefill launcher sets it (K-sliced plain products write several partials)
     }
+    return l;
+}
+
+extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
+    if (!ctx || !m) return fail(QH_EINVAL, "split: null");
+    if (n == 0) return 1;
+    if (n <= (size_t)SKINNY_MAX_M) return skinny_partition(ctx, m, n, true).split;
+    if (n > (size_t)PF_KS_MAX_M || n > (1u << 24)) return 1;
+    Launch l = make_launch(ctx, m, nullptr, m->cols, n, nullptr, nullptr, QH_EPI_PLAIN, nullptr, 0, nullptr);
+    l.dry_run = 1;
+    if (hipError_t e = launch(l); e != hipSuccess) return fail(QH_EHIP, "split: %s", hipGetErrorString(e));
+    return l.split;
+}
+
+extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok) {
+    size_t len = 0;
+    for (size_t i = 0; ctx && mats && i < count; i++) {
+        if (!mats[i]) continue;
+        // decode sizes: the skinny partition's split (the same for every token count); prefill sizes up to
+        // PF_KS_MAX_M tokens: at most PF_KS_MAX partials; beyond: one
+        size_t rows = std::max({max_tok, (size_t)qh_mat_split(ctx, mats[i], 1) * std::min(max_tok, (size_t)SKINNY_MAX_M),
+                                (size_t)PF_KS_MAX * std::min(max_tok, (size_t)PF_KS_MAX_M)});
+        len = std::max(len, rows * mats[i]->rows);
+    }
+    return len;
+}
+
+extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
+                       const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
+    if (!ctx || !w || !x || !y) return fail(QH_EINVAL, "gemm: null");
+    if (epi != QH_EPI_PLAIN && epi != QH_EPI_SILU && epi != QH_EPI_ARGMAX) return fail(QH_EINVAL, "epilogue %d", epi);
+    if (epi == QH_EPI_ARGMAX && !keys) return fail(QH_EINVAL, "argmax without keys");
+    if (epi == QH_EPI_SILU && w->rows % 16) return fail(QH_EINVAL, "SwiGLU of %zu rows", w->rows);
+    if (ldx == 0) ldx = w->cols;
+    if (ldx < w->cols || ldx % 8 || (uintptr_t)x % 16)
+        return fail(QH_EINVAL, "x rows of %zu elements at %p: 16-byte aligned rows of at least %zu", ldx, x, w->cols);
+    const size_t m = epi == QH_EPI_ARGMAX ? n_out : n;
+    if (m == 0) return 1;
+    if (epi == QH_EPI_ARGMAX && m > (size_t)ARGMAX_MAX_TOK)
+        return fail(QH_EINVAL, "argmax over %zu logit rows: at most %d", m, ARGMAX_MAX_TOK);
+    if (m > (1u << 24) || w->rows > (1u << 30) || ldx > (1u << 30)) return fail(QH_EINVAL, "gemm: sizes too large");
+    // the prefill kernel addresses activation rows (the n token rows, also those the argmax gathers) with 32-bit byte
+    // offsets from x
+    if (m > (size_t)SKINNY_MAX_M && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
+        return fail(QH_EINVAL, "gemm: %zu token rows of %zu elements: x must fit in 4 GiB", n, ldx);
+    Launch l = make_launch(ctx, w, x, ldx, m, out_rows, y, epi, keys, whole, stream);
     hipError_t e = launch(l);
     if (e != hipSuccess) return fail(QH_EHIP, "gemm launch: %s", hipGetErrorString(e));
     return l.split;

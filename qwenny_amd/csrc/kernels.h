@@ -46,6 +46,9 @@ struct Launch {
     unsigned* sk_count;
     int stream_k;
     int dp_items, sk_items, sk_wgs, sk_q, sk_r;
+    // plain prefill products of few tokens: whole items cut into ks slices of K, slice s writing partial y[s] (the
+    // split-K contract; ks = 1: none). whole: the caller wants one partial. dry_run: plan only (l.split), no launch.
+    int ks, whole, dry_run;
     uint32_t bf16_magic;    // 0x43004300: the bf16 pair (128, 128) (see kernels.hip i4_biased)
     uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;
@@ -61,6 +64,11 @@ constexpr size_t PF_SK_PART_BYTES = (size_t)128 << 20;
 constexpr int PF_SK_ITEMS_MAX = 4096;
 // Cost of stream-K's partials in units of one group's compute (the launcher's choice between whole items and stream-K).
 constexpr int PF_SK_FIXUP = 12;
+// K slices of plain prefill products (at most PF_KS_MAX, up to PF_KS_MAX_M tokens), and the estimated cost of a slice's
+// extra pipeline start and partial, in the same units.
+constexpr int PF_KS_MAX = 4;
+constexpr int PF_KS_MAX_M = 384;
+constexpr int PF_KS_COST = 2;
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
 constexpr int SKINNY_MAX_M = 48;  // the skinny kernel up to 48 tokens (three 16-token blocks per MFMA pass)
@@ -80,9 +88,9 @@ enum { EPI_PLAIN = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
 // The kernels of one storage format F and epilogue EPI: the skinny kernel for m <= SKINNY_MAX_M, else the prefill
 // kernel.
 template <int F, int EPI>
-hipError_t launch_epi(const Launch& l);
+hipError_t launch_epi(Launch& l);
 
-// launch_epi for l.fmt and l.epi.
-hipError_t launch(const Launch& l);
+// launch_epi for l.fmt and l.epi; sets l.split to the partials the launch writes.
+hipError_t launch(Launch& l);
 
 }  // namespace qh

@@ -496,6 +496,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     const int nwt = (tiles + WTILES - 1) / WTILES;  // weight tiles (of WTILES 16-row tiles); items: weight tiles fastest
     const int wtok0 = wm * BMB * 32;  // the wave's first token row in the stage
     int tok0 = 0, tile0 = 0;          // the current item's first token and the wave's first tile
+    int kslice = 0;                   // the partial a K-sliced whole item writes (a.ks > 1)
 
     // Global loads take a wave-uniform base plus a 32-bit per-lane byte offset fixed for the item (no 64-bit address
     // arithmetic per load).
@@ -674,7 +675,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
                             ((__bf16*)a.y)[(size_t)tok * a.ldy + tile * 8 + l16] = (__bf16)(silu(val) * up);
                     } else {
                         // streamed past the caches: the outputs are not read again here, the tiles still are
-                        if (tile_ok && tok < M) __builtin_nontemporal_store(val, (float*)a.y + (size_t)tok * a.ldy + out);
+                        if (tile_ok && tok < M)
+                            __builtin_nontemporal_store(val, (float*)a.y + ((size_t)kslice * M + tok) * a.ldy + out);
                         if (EPI == EPI_ARGMAX && tile_ok && tok < M && out < a.valid)
                             key[bb][v] = max_u64(key[bb][v], argmax_key(val, out));
                     }
@@ -700,9 +702,16 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     const int b = blockIdx.x, dp = a.dp_items;
     int u, u1, s = -1;
     if (b < dp) {
-        const int xcd = b & 7, q8 = dp >> 3, r8 = dp & 7;
-        u = (xcd * q8 + min(xcd, r8) + (b >> 3)) * G;
-        u1 = u + G;
+        const int xcd = b & 7, q8 = dp >> 3, r8 = dp & 7, ui = xcd * q8 + min(xcd, r8) + (b >> 3);
+        if (a.ks > 1) {  // slice kslice of K of item ui / ks, written as partial kslice
+            const int item = ui / a.ks;
+            kslice = ui - item * a.ks;
+            u = item * G + kslice * G / a.ks;
+            u1 = item * G + (kslice + 1) * G / a.ks;
+        } else {
+            u = ui * G;
+            u1 = u + G;
+        }
     } else {
         // stream-K range s, XCD-aware like whole items: workgroups b and b + 8 run on one XCD, and each XCD takes a
         // contiguous run of ranges (so the items they cut share its L2)
@@ -725,7 +734,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         set_item(it);
         run(g0, g1);
         u += g1 - g0;
-        if (g0 != 0 || g1 != G) {
+        if (a.ks == 1 && (g0 != 0 || g1 != G)) {
             // a cut item (stream-K): write this segment's partial to slot 2 s (+1 unless it is this workgroup's
             // first item), as [wave][register / 4][lane][4] f32, with 16-byte device-coherent stores
             const uint32_t part = sk_off(2 * s + (it != first_item), wave, lane);
@@ -817,6 +826,8 @@ static hipError_t skinny_epi(const Launch& l) {
 // K = 5120 stays whole).
 template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB = 1>
 static long prefill_plan(Launch& l) {
+    l.ks = 1;
+    l.split = 1;
     const int tiles = l.rows / TILE, G = l.cols / QG;
     const int wg_tiles = WN * TN * 2, bm = WM * BMB * 32, threads = WM * WN * 64;
     const long items = (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
@@ -847,15 +858,28 @@ static long prefill_plan(Launch& l) {
         l.sk_wgs = (int)P;
         l.sk_q = (int)(U / P);
         l.sk_r = (int)(U % P);
-        return t_sk;
     }
-    return t_dp;
+    long t = l.sk_items ? t_sk : t_dp;
+    // plain products of few tokens: K slices of whole items, each writing a partial (no stream-K fix-up)
+    if (EPI == EPI_PLAIN && !l.whole && l.m <= PF_KS_MAX_M)
+        for (int ks = 2; ks <= PF_KS_MAX && ks <= G; ks *= 2) {
+            const long units = items * ks, t_ks = (units + P - 1) / P * ((G + ks - 1) / ks) + PF_KS_COST;
+            if (t_ks < t && units < (1l << 31)) {
+                t = t_ks;
+                l.ks = ks;
+                l.split = ks;
+                l.dp_items = (int)units;
+                l.sk_items = 0;
+                l.sk_wgs = 0;
+            }
+        }
+    return t;
 }
 
 template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB = 1>
-static hipError_t prefill_cfg(const Launch& l0) {
-    Launch l = l0;
+static hipError_t prefill_cfg(Launch& l) {
     (void)prefill_plan<F, EPI, BMB, TN, WM, WN, MINB>(l);
+    if (l.dry_run) return hipSuccess;
     hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>), dim3(l.dp_items + l.sk_wgs),
                        dim3(WM * WN * 64), 0, l.stream, l);
     return hipGetLastError();
@@ -865,7 +889,7 @@ static hipError_t prefill_cfg(const Launch& l0) {
 // on 12 waves when that fills the CUs better), else 128 x 128 on 4 waves, else 64 x 128 on 4 waves; QH_PF_SHAPE forces
 // one in tuning sweeps (256 x 128 on 4 waves, 1, and the wider wave tiles 3 and 4 only then).
 template <int F, int EPI>
-static hipError_t prefill_epi(const Launch& l) {
+static hipError_t prefill_epi(Launch& l) {
     const int tiles = l.rows / TILE;
     auto items = [&](int bm, int wg_tiles) {
         return (long)((tiles + wg_tiles - 1) / wg_tiles) * ((l.m + bm - 1) / bm);
@@ -886,6 +910,7 @@ static hipError_t prefill_epi(const Launch& l) {
             // 3/4 the work at about 0.85 of the rate of 256 x 256: (5120, 6144) at 2048 tokens fills all 256 CUs with
             // it, 3/4 of them with 256 x 256, measured +10%)
             Launch a = l, b = l;
+            a.dry_run = b.dry_run = 1;
             if (prefill_plan<F, EPI, 4, 1, 2, 6>(a) * 15 < prefill_plan<F, EPI, 8, 1, 1, 8>(b) * 17) shape = 7;
         } else if (l.m > 64 && items(128, 8) * 4 >= l.cus && pads_ok(128)) shape = 5;
         else shape = 6;
@@ -905,11 +930,11 @@ static hipError_t prefill_epi(const Launch& l) {
 // This object holds the kernels of one (format, epilogue) pair: the library compiles kernels.hip once per pair, in
 // parallel, plus once with QH_PART_DISPATCH for the dispatcher.
 template <int F, int EPI>
-hipError_t launch_epi(const Launch& l) {
-    if (l.m <= SKINNY_MAX_M) return skinny_epi<F & ~F_PERCH, EPI>(l);
+hipError_t launch_epi(Launch& l) {
+    if (l.m <= SKINNY_MAX_M) return l.dry_run ? hipSuccess : skinny_epi<F & ~F_PERCH, EPI>(l);
     return prefill_epi<F, EPI>(l);
 }
-template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(const Launch& l);
+template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(Launch& l);
 #endif
 
 #ifdef QH_PART_DISPATCH
@@ -920,7 +945,7 @@ size_t skinny_lds(const Launch& l) {
 }
 
 template <int F>
-static hipError_t launch_fmt(const Launch& l) {
+static hipError_t launch_fmt(Launch& l) {
     switch (l.epi) {
         case EPI_SILU: return launch_epi<F, EPI_SILU>(l);
         case EPI_ARGMAX: return launch_epi<F, EPI_ARGMAX>(l);
@@ -928,7 +953,7 @@ static hipError_t launch_fmt(const Launch& l) {
     }
 }
 
-hipError_t launch(const Launch& l) {
+hipError_t launch(Launch& l) {
     switch (l.fmt) {
         case F_I4: return launch_fmt<F_I4>(l);
         case F_I4 | F_S32: return launch_fmt<F_I4 | F_S32>(l);

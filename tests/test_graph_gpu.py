@@ -29,7 +29,7 @@ def test_graph_replays_match_eager(gemm):
     y_dec = torch.empty((split, m_dec, dec.rows), dtype=torch.float32, device="cuda")
     y_head = torch.empty((m_dec, head.rows), dtype=torch.float32, device="cuda")
     keys = torch.zeros(m_dec, dtype=torch.int64, device="cuda")
-    y_pre = torch.empty((1, m_pre, pre.rows), dtype=torch.float32, device="cuda")
+    y_pre = torch.empty((pre.split(m_pre), m_pre, pre.rows), dtype=torch.float32, device="cuda")
 
     def step(stream):
         gemm.run(stream, m_dec, dec, x_dec, y_dec, Epi.Plain)

@@ -30,7 +30,8 @@ def test_shape_256x192_stream_k_plain(gemm, kind):
     for rep in range(2):  # the item counters must be left at zero by each launch
         x = activations(121 + rep, "x", m, k, outliers=0.01)
         y = torch.full((1, m, n), float("nan"), dtype=torch.float32, device="cuda")
-        assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == 1
+        # one partial (whole): the stream-K path, not the K-sliced partials of a short plain product
+        assert gemm.run_split(None, m, mat, to_dev(x), y, Epi.Plain, True) == 1
         torch.cuda.synchronize()
         got = y[0].cpu().numpy().astype(np.float64)
         assert not np.isnan(got).any()
@@ -69,7 +70,7 @@ def test_shape_256x192_dense_bf16(gemm):
     mat = Mat.new(gemm, w, k, int8=False)
     x = activations(141, "x", m, k, outliers=0.01)
     y = torch.full((1, m, n), float("nan"), dtype=torch.float32, device="cuda")
-    assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == 1
+    assert gemm.run_split(None, m, mat, to_dev(x), y, Epi.Plain, True) == 1
     torch.cuda.synchronize()
     got = y[0].cpu().numpy().astype(np.float64)
     assert not np.isnan(got).any()

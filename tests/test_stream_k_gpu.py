@@ -23,7 +23,8 @@ def _run_plain(gemm, mat, x, m):
     import torch
 
     y = torch.full((1, m, mat.rows), float("nan"), dtype=torch.float32, device="cuda")
-    assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == 1
+    # one partial (whole): short plain products otherwise take K-sliced partials instead of stream-K
+    assert gemm.run_split(None, m, mat, to_dev(x), y, Epi.Plain, True) == 1
     torch.cuda.synchronize()
     return y[0].cpu().numpy().astype(np.float64)
 
@@ -75,3 +76,30 @@ def test_stream_k_silu(gemm):
     full = np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
     want = oracle.silu_glu(full, row_order(n, True))
     assert bf16_out_err(y.float().cpu().numpy(), want) <= 1e-3
+
+
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
+@pytest.mark.parametrize("m", [49, 130, 256, 384])
+def test_k_sliced_plain(gemm, kind, m):
+    """Short plain prefill products write K-sliced partials (whole items cut into 2-4 slices of K, slice s into
+    y[s]) instead of stream-K: the returned split matches qh_mat_split, every partial is written, and their sum is the
+    product (the oracle to 2e-2 RMS, the kernel's own arithmetic to 1e-4)."""
+    import torch
+
+    print(f"K-sliced plain {kind} m={m}", flush=True)
+    n, k = 6144, 5120
+    q = make_quant(180 + m, kind, n, k)
+    mat = Mat.stack(gemm, [q])
+    split = mat.split(m)
+    rows = np.sort(np.random.default_rng(m).choice(n, 256, replace=False))
+    sq = sub_quant(q, rows)
+    for rep in range(2):
+        x = activations(181 + rep, "x", m, k, outliers=0.01)
+        y = torch.full((split, m, n), float("nan"), dtype=torch.float32, device="cuda")
+        assert gemm.run(None, m, mat, to_dev(x), y, Epi.Plain) == split
+        torch.cuda.synchronize()
+        parts = y.cpu().numpy().astype(np.float64)
+        assert not np.isnan(parts).any()
+        got = parts.sum(0)[:, rows]
+        assert rel_err(got, oracle_y(sq, x)) <= TOL, rep
+        assert rel_err(got, emulate_bf16_weights(sq, x)) <= 1e-4, rep
