@@ -67,8 +67,10 @@ constexpr int PF_SK_FIXUP = 12;
 // K slices of plain prefill products (at most PF_KS_MAX, up to PF_KS_MAX_M tokens), and the estimated cost of a slice's
 // extra pipeline start and partial, in the same units.
 constexpr int PF_KS_MAX = 4;
-constexpr int PF_KS_MAX_M = 384;
+constexpr int PF_KS_MAX_M = 512;
 constexpr int PF_KS_COST = 2;
+// The rates that price the slices' extra partials in those units: one CU's MFMA rate under load, and HBM.
+constexpr double PF_KS_CU_FLOPS = 4e12, PF_KS_HBM = 5e12;
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
 constexpr int SKINNY_MAX_M = 48;  // the skinny kernel up to 48 tokens (three 16-token blocks per MFMA pass)

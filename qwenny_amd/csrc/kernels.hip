@@ -863,7 +863,13 @@ static long prefill_plan(Launch& l) {
     // plain products of few tokens: K slices of whole items, each writing a partial (no stream-K fix-up)
     if (EPI == EPI_PLAIN && !l.whole && l.m <= PF_KS_MAX_M)
         for (int ks = 2; ks <= PF_KS_MAX && ks <= G; ks *= 2) {
-            const long units = items * ks, t_ks = (units + P - 1) / P * ((G + ks - 1) / ks) + PF_KS_COST;
+            // the extra partials (ks - 1 more f32 outputs per token and row, written here and read back by the
+            // consumer) at PF_KS_HBM bytes/s, in units of one group of one item on a CU running per_cu of them at
+            // PF_KS_CU_FLOPS
+            const double unit_s = 2.0 * bm * wg_tiles * TILE * QG * per_cu / PF_KS_CU_FLOPS;
+            const double extra_s = (double)(ks - 1) * l.m * l.rows * 8 / PF_KS_HBM;
+            const long units = items * ks,
+                       t_ks = (units + P - 1) / P * ((G + ks - 1) / ks) + PF_KS_COST + (long)(extra_s / unit_s + 0.5);
             if (t_ks < t && units < (1l << 31)) {
                 t = t_ks;
                 l.ks = ks;

@@ -79,7 +79,7 @@ def test_stream_k_silu(gemm):
 
 
 @pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
-@pytest.mark.parametrize("m", [49, 130, 256, 384])
+@pytest.mark.parametrize("m", [49, 130, 256, 512])
 def test_k_sliced_plain(gemm, kind, m):
     """Short plain prefill products write K-sliced partials (whole items cut into 2-4 slices of K, slice s into
     y[s]) instead of stream-K: the returned split matches qh_mat_split, every partial is written, and their sum is the
