@@ -395,6 +395,44 @@ def consumers_line(args):
     return {"consumers": out}
 
 
+class SummedStep(Step):
+    """A Step of one plain product followed by the sum of its split partials (`sum_parts`), so that products that
+    return several partials are timed with the consumer's read of them."""
+
+    def __init__(self, gemm, m, kmax, mat):
+        import torch
+
+        super().__init__(gemm, m, kmax)
+        self.split = mat.split(m)
+        self.sum = torch.empty(m * mat.rows, dtype=torch.float32, device="cuda")
+
+    def run(self, stream=None):
+        from qwenny_amd import sum_parts
+
+        super().run(stream)
+        mat, _, y, _, _ = self.launches[0]
+        sum_parts(stream, y, self.split, self.m, mat.rows, self.sum)
+
+
+def short_prefill_line(gemm, set_mats, args):
+    """Plain int4 products of 64, 256 and 512 tokens on the 27B prefill shapes (K slices or stream-K, whichever the
+    launcher picks), each with the sum of its partials, in HIP graphs: TFLOP/s of the product and the split used."""
+    from qwenny_amd import Epi
+
+    out = {}
+    for m in (64, 256, 512):
+        for i, (k, n) in enumerate(PREFILL_27B):
+            mat = set_mats[[0, 2, 3][i]][0]
+            st = SummedStep(gemm, m, k, mat)
+            st.add(mat, Epi.Plain, int4_bytes(k, n, m), 2 * m * k * n)
+            ms = time_step(st, max(50, args.steps), 5, not args.no_graph)
+            tf = st.flops() / (ms * 1e-3) / 1e12
+            out[f"m{m}_{k}x{n}"] = {"TFLOPs": round(tf, 1), "split": st.split}
+            print(f"# prefill + sum M={m} K={k} N={n}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s, split {st.split}",
+                  file=sys.stderr, flush=True)
+    return {"prefill_short_TFLOPs": out}
+
+
 def summarize_clock(pmc_dir, min_ns=50000):
     """Per kernel (name, grid) of a rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES run: mean duration, the
     clock it ran at (GRBM_GUI_ACTIVE sums the 8 XCDs' cycles) and the fraction of cycles each SIMD's MFMA unit was busy
@@ -432,7 +470,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,int8,dense,dequant,set4b,consumers")
+    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,pfshort,int8,dense,dequant,set4b,consumers")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -462,7 +500,7 @@ def main():
 
     torch.cuda.init()
     gemm = Gemm.load(0)
-    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "int8", "dense", "dequant", "set4b", "consumers"}
+    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "pfshort", "int8", "dense", "dequant", "set4b", "consumers"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
@@ -531,6 +569,8 @@ def main():
             print(f"# prefill M=2048 K={k} N={n}: {msp:.3f} ms, {tf:.1f} TFLOP/s ({tf / BF16_PEAK:.1%})",
                   file=sys.stderr, flush=True)
         extra["prefill_m2048_TFLOPs"] = pf
+    if "pfshort" in only:
+        extra.update(short_prefill_line(gemm, set_mats, args))
     if "int8" in only:
         i8 = [upload_copies(gemm, quant(300 + i, "i8", k, n), 4) for i, (k, n) in
               enumerate([(5120, 17408), (17408, 5120)])]
