@@ -172,7 +172,7 @@ int qh_mat_describe(const qh_mat* m, qh_mat_desc* out);
 int qh_mat_download(const qh_mat* m, void* codes, void* scales, void* zeros);
 
 /* Split-K factor a plain product of n tokens uses on m (core.rs Mat::split): the skinny kernel's K chunks up to 48
- * tokens, 1, 2 or 4 K slices for 49-512, 1 above. No launch; the same value qh_gemm returns. */
+ * tokens, 1-16 K slices (slices x tokens <= 2048) for 49-512, 1 above. No launch; the same value qh_gemm returns. */
 int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n);
 
 /* part_len (core.rs:315-318): floats the plain products of `mats` write at most, for up to `max_tok` tokens. */

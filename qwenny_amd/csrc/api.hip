@@ -361,9 +361,9 @@ extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size
     for (size_t i = 0; ctx && mats && i < count; i++) {
         if (!mats[i]) continue;
         // decode sizes: the skinny partition's split (the same for every token count); prefill sizes up to
-        // PF_KS_MAX_M tokens: at most PF_KS_MAX partials; beyond: one
+        // PF_KS_MAX_M tokens: at most PF_KS_MAX partials and PF_KS_ROWS partial rows; beyond: one
         size_t rows = std::max({max_tok, (size_t)qh_mat_split(ctx, mats[i], 1) * std::min(max_tok, (size_t)SKINNY_MAX_M),
-                                (size_t)PF_KS_MAX * std::min(max_tok, (size_t)PF_KS_MAX_M)});
+                                std::min((size_t)PF_KS_MAX * std::min(max_tok, (size_t)PF_KS_MAX_M), (size_t)PF_KS_ROWS)});
         len = std::max(len, rows * mats[i]->rows);
     }
     return len;

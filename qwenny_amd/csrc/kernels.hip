@@ -862,7 +862,8 @@ static long prefill_plan(Launch& l) {
     long t = l.sk_items ? t_sk : t_dp;
     // plain products of few tokens: K slices of whole items, each writing a partial (no stream-K fix-up)
     if (EPI == EPI_PLAIN && !l.whole && l.m <= PF_KS_MAX_M)
-        for (int ks = 2; ks <= PF_KS_MAX && ks <= G; ks *= 2) {
+        for (int ks = 2; ks <= PF_KS_MAX && ks <= G && (ks <= 4 || G / ks >= PF_KS_MIN_G) && (long)ks * l.m <= PF_KS_ROWS;
+             ks *= 2) {
             // the extra partials (ks - 1 more f32 outputs per token and row, written here and read back by the
             // consumer) at PF_KS_HBM bytes/s, in units of one group of one item on a CU running per_cu of them at
             // PF_KS_CU_FLOPS

@@ -148,8 +148,8 @@ def test_part_len(gemm):
     for max_tok in (16, SKINNY_MAX_M, SKINNY_MAX_M + 1, 300, 600):
         need = max(m.split(n) * n * m.rows for m in mats for n in range(1, max_tok + 1))
         assert gemm.part_len(mats, max_tok) >= need, max_tok
-    # decode sizes: one partial per 4 groups of K; short prefill: up to 4 K slices; from 513 tokens: one
-    assert mats[1].split(SKINNY_MAX_M) > 4 and 1 <= mats[1].split(SKINNY_MAX_M + 1) <= 4 and mats[1].split(513) == 1
+    # decode sizes: one partial per 4 groups of K; short prefill: up to 16 K slices; from 513 tokens: one
+    assert mats[1].split(SKINNY_MAX_M) > 4 and 1 <= mats[1].split(SKINNY_MAX_M + 1) <= 16 and mats[1].split(513) == 1
 
 
 def test_checkpoint_end_to_end(gemm, tmp_path):

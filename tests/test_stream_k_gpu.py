@@ -79,15 +79,15 @@ def test_stream_k_silu(gemm):
 
 
 @pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
-@pytest.mark.parametrize("m", [49, 130, 256, 512])
-def test_k_sliced_plain(gemm, kind, m):
-    """Short plain prefill products write K-sliced partials (whole items cut into 2-4 slices of K, slice s into
+@pytest.mark.parametrize("m", [49, 64, 130, 256, 512])
+@pytest.mark.parametrize("n,k", [(6144, 5120), (5120, 17408)])
+def test_k_sliced_plain(gemm, kind, m, n, k):
+    """Short plain prefill products write K-sliced partials (whole items cut into 2-16 slices of K, slice s into
     y[s]) instead of stream-K: the returned split matches qh_mat_split, every partial is written, and their sum is the
     product (the oracle to 2e-2 RMS, the kernel's own arithmetic to 1e-4)."""
     import torch
 
-    print(f"K-sliced plain {kind} m={m}", flush=True)
-    n, k = 6144, 5120
+    print(f"K-sliced plain {kind} m={m} {n}x{k}", flush=True)
     q = make_quant(180 + m, kind, n, k)
     mat = Mat.stack(gemm, [q])
     split = mat.split(m)
