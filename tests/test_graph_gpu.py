@@ -22,9 +22,12 @@ def test_graph_replays_match_eager(gemm):
     dec = Mat.stack(gemm, [make_quant(91, "i4", 2048, k)])       # skinny, split-K partials
     head = Mat.stack(gemm, [make_quant(92, "i4z", 8192, k)])     # skinny, argmax across workgroups
     pre = Mat.stack(gemm, [make_quant(93, "i4", 4096, k)])       # prefill at 256 tokens: items spread (stream-K)
-    m_dec, m_pre = 1, 256
+    sl = Mat.stack(gemm, [make_quant(94, "i4", 1024, k)])        # prefill at 64 tokens: K-sliced partials
+    m_dec, m_pre, m_sl = 1, 256, 64
+    assert sl.split(m_sl) > 1
     x_dec = torch.empty((m_dec, k), dtype=torch.bfloat16, device="cuda")
     x_pre = torch.empty((m_pre, k), dtype=torch.bfloat16, device="cuda")
+    y_sl = torch.empty((sl.split(m_sl), m_sl, sl.rows), dtype=torch.float32, device="cuda")
     split = dec.split(m_dec)
     y_dec = torch.empty((split, m_dec, dec.rows), dtype=torch.float32, device="cuda")
     y_head = torch.empty((m_dec, head.rows), dtype=torch.float32, device="cuda")
@@ -35,10 +38,11 @@ def test_graph_replays_match_eager(gemm):
         gemm.run(stream, m_dec, dec, x_dec, y_dec, Epi.Plain)
         gemm.run(stream, m_dec, head, x_dec, y_head, Epi.Argmax, n_out=m_dec, keys=keys)
         gemm.run(stream, m_pre, pre, x_pre, y_pre, Epi.Plain)
+        gemm.run(stream, m_sl, sl, x_pre, y_sl, Epi.Plain)  # the first 64 tokens of x_pre
 
     def outputs():
         return y_dec.sum(0).cpu().numpy(), y_head.cpu().numpy(), keys.cpu().numpy().view(np.uint64).copy(), \
-            y_pre.cpu().numpy()
+            y_pre.cpu().numpy(), y_sl.cpu().numpy()
 
     def load_inputs(seed):
         x_dec.copy_(to_dev(activations(seed, "x", m_dec, k)))
@@ -64,6 +68,7 @@ def test_graph_replays_match_eager(gemm):
         y_dec.fill_(float("nan"))
         y_head.fill_(float("nan"))
         y_pre.fill_(float("nan"))
+        y_sl.fill_(float("nan"))
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
