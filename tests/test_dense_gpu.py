@@ -48,6 +48,20 @@ def test_dense_plain(gemm, m):
     assert rel_err(got, oracle.dense_f64(w, x, f16_weights=True)) <= TOL
 
 
+@pytest.mark.parametrize("m", [64, 200])
+def test_dense_k_sliced(gemm, m):
+    """A short dense prefill product cut into K slices: several partials, each written, summing to the product."""
+    print(f"dense K-sliced m={m}", flush=True)
+    rows, cols = 1024, 4096
+    w = _weights(56 + m, rows, cols)
+    x = activations(57 + m, "x", m, cols, outliers=0.01)
+    mat = Mat.new(gemm, w, cols, int8=False)
+    assert mat.split(m) > 1
+    got = _plain(gemm, mat, x, m)
+    assert not np.isnan(got).any()
+    assert rel_err(got, oracle.dense_f64(w, x)) <= 1e-4
+
+
 @pytest.mark.parametrize("m", [1, 5, 300])
 def test_dense_in_ba_shape(gemm, m):
     """The 27B DeltaNet in_ba projection (K 5120, N 96), which stays 16-bit in a pre-quantized checkpoint: 6 tiles,
