@@ -58,10 +58,11 @@ def test_lora_add_matches_oracle(gemm, rank, split, n, m_cols):
     assert (got[:, 64:128] == y0[:, 64:128]).all()
 
 
-@pytest.mark.parametrize("m", [1, 5, 40])
+@pytest.mark.parametrize("m", [1, 5, 40, 64, 200])
 def test_lora_add_end_to_end(gemm, m):
     """y = W x + s B (A x): W int4 (1024 x 512) as plain split-K partials, xa = A x from a dense bf16 A of two rank-16
-    modules (32 rows), the delta on split 0 of the product, then the partials summed."""
+    modules (32 rows), the delta on split 0 of the product, then the partials summed. At 64 and 200 tokens both
+    products are K-sliced prefill products (4 partials each)."""
     import torch
 
     print(f"lora_add end to end m={m}", flush=True)
