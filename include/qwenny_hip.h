@@ -75,6 +75,8 @@ typedef struct qh_mat_desc {
     size_t code_bytes;  /* device bytes of the packed codes */
     size_t scale_bytes; /* device bytes of the scales */
     size_t zero_bytes;  /* device bytes of the zero points (0 unless QH_WT_I4Z or QH_WT_I4Z_S32) */
+    int32_t per_channel; /* QH_WT_I8 with one scale per row (every group's equal): prefill products in exact
+                          * integers with the row's scale after the sum; 0: a scale per row and 128 columns */
 } qh_mat_desc;
 
 /* The last error of the calling thread ("" if none). */

@@ -21,7 +21,7 @@ class MatDesc(ctypes.Structure):
     """qh_mat_desc"""
 
     _fields_ = [("wt", ctypes.c_int32), ("rows", S), ("cols", S), ("valid", S), ("code_bytes", S),
-                ("scale_bytes", S), ("zero_bytes", S)]
+                ("scale_bytes", S), ("zero_bytes", S), ("per_channel", ctypes.c_int32)]
 
 
 # name -> (restype, argtypes); every symbol include/qwenny_hip.h declares

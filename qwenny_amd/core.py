@@ -215,6 +215,11 @@ class Mat:
         return Wt(self.desc().wt)
 
     @property
+    def per_channel(self):
+        """int8 with one scale per row: prefill products in exact integers, the row's scale after the sum."""
+        return bool(self.desc().per_channel)
+
+    @property
     def rows(self):
         return self.desc().rows
 

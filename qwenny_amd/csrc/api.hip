@@ -240,7 +240,8 @@ extern "C" int qh_mat_dense(qh_ctx* ctx, const uint16_t* bf16, size_t rows, size
 
 extern "C" int qh_mat_describe(const qh_mat* m, qh_mat_desc* out) {
     if (!m || !out) return fail(QH_EINVAL, "describe: null");
-    *out = qh_mat_desc{m->wt, m->rows, m->cols, m->valid, m->code_bytes, m->scale_bytes, m->zero_bytes};
+    *out = qh_mat_desc{m->wt, m->rows, m->cols, m->valid, m->code_bytes, m->scale_bytes, m->zero_bytes,
+                       m->per_channel ? 1 : 0};
     return QH_OK;
 }
 

@@ -77,10 +77,11 @@ def int4_quant(seed, name, n, k, zp=False, group=128):
     return t
 
 
-def int8_quant(seed, name, n, k):
-    """A synthetic per-channel int8 matrix (strategy "channel": one scale per row) -> compressed-tensors tensors."""
+def int8_quant(seed, name, n, k, group=0):
+    """A synthetic int8 matrix -> compressed-tensors tensors: per channel (group 0, strategy "channel": one scale per
+    row, U(0.001, 0.01)) or per group of `group` columns (strategy "group", scales U(0.001, 0.01) per row and group)."""
     return {
         "weight_packed": int8_packed(seed, name, n, k),
-        "weight_scale": scales_bf16(seed, name, (n, 1), 0.001, 0.01),
+        "weight_scale": scales_bf16(seed, name, (n, k // group if group else 1), 0.001, 0.01),
         "weight_shape": np.array([n, k], np.int64),
     }

@@ -13,11 +13,13 @@ TOL = 2e-2
 
 
 def make_quant(seed, kind, n, k, group=128):
-    """A synthetic stored matrix: kind 'i4' (symmetric), 'i4z' (packed zero points), 'i8' (per-channel int8)."""
+    """A synthetic stored matrix: kind 'i4' (symmetric), 'i4z' (packed zero points), 'i8' (per-channel int8),
+    'i8g' (int8 with a scale per row and `group` columns)."""
     name = f"{kind}_{n}_{k}"
-    if kind == "i8":
-        t = synth.int8_quant(seed, name, n, k)
-        return quant_from_packed(t["weight_packed"], synth.bf16_to_f32(t["weight_scale"]), 8, 0, None,
+    if kind in ("i8", "i8g"):
+        g = group if kind == "i8g" else 0
+        t = synth.int8_quant(seed, name, n, k, group=g)
+        return quant_from_packed(t["weight_packed"], synth.bf16_to_f32(t["weight_scale"]), 8, g, None,
                                  t["weight_shape"])
     t = synth.int4_quant(seed, name, n, k, zp=kind == "i4z", group=group)
     return quant_from_packed(t["weight_packed"], synth.bf16_to_f32(t["weight_scale"]), 4, group,

@@ -74,7 +74,7 @@ def test_config2_27b_set_and_head(gemm, m):
     assert (np.argmax(logits, axis=1) == np.argmax(want, axis=1)).all()
 
 
-@pytest.mark.parametrize("m", [256, 2048])
+@pytest.mark.parametrize("m", [256, 512, 2048])
 @pytest.mark.parametrize("kind", ["i4", "i4z"])
 def test_config3_prefill(gemm, m, kind):
     print(f"configs[3] prefill {kind} m={m}", flush=True)

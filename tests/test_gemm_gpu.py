@@ -18,8 +18,10 @@ from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, 
 
 pytestmark = pytest.mark.gpu
 
-KINDS = ["i4", "i4z", "i8"]
-WT_OF = {"i4": Wt.I4, "i4z": Wt.I4Z, "i8": Wt.I8}
+# i8: int8 per channel (exact integer prefill); i8g: int8 with a scale per row and 128 columns (the reference's
+# default load mode, dequantized per group in the prefill kernel)
+KINDS = ["i4", "i4z", "i8", "i8g"]
+WT_OF = {"i4": Wt.I4, "i4z": Wt.I4Z, "i8": Wt.I8, "i8g": Wt.I8}
 
 
 def _plain(gemm, mat, x, m, stream=None):
@@ -51,6 +53,7 @@ def test_skinny_plain(gemm, kind, m):
     x = activations(5 + m, "x", m, 1024)
     mat = Mat.stack(gemm, [q])
     assert mat.wt == WT_OF[kind]
+    assert mat.per_channel == (kind == "i8")
     _check(_plain(gemm, mat, x, m), q, x, m)
 
 
@@ -61,6 +64,7 @@ def test_prefill_plain(gemm, kind, m):
     q = make_quant(21 + m, kind, 384, 768)
     x = activations(6 + m, "x", m, 768, outliers=0.01)
     mat = Mat.stack(gemm, [q])
+    assert mat.per_channel == (kind == "i8")
     _check(_plain(gemm, mat, x, m), q, x, m)
 
 

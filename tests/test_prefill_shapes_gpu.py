@@ -17,7 +17,7 @@ from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8", "i8g"])
 def test_shape_256x192_stream_k_plain(gemm, kind):
     import torch
 

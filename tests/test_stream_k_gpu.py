@@ -29,7 +29,7 @@ def _run_plain(gemm, mat, x, m):
     return y[0].cpu().numpy().astype(np.float64)
 
 
-@pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8", "i8g"])
 @pytest.mark.parametrize("m", [130, 256])
 def test_stream_k_plain(gemm, kind, m):
     print(f"stream-K plain {kind} m={m}", flush=True)
@@ -78,7 +78,7 @@ def test_stream_k_silu(gemm):
     assert bf16_out_err(y.float().cpu().numpy(), want) <= 1e-3
 
 
-@pytest.mark.parametrize("kind", ["i4", "i4z", "i8"])
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8", "i8g"])
 @pytest.mark.parametrize("m", [49, 64, 130, 256, 512])
 @pytest.mark.parametrize("n,k", [(6144, 5120), (5120, 17408)])
 def test_k_sliced_plain(gemm, kind, m, n, k):
