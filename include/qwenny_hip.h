@@ -192,6 +192,16 @@ size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, s
 int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, const int32_t* out_rows,
             size_t n_out, void* y, int epi, uint64_t* keys, int whole);
 
+/* qh_gemm without allocation: no counterpart in the reference. For callers that cannot allocate device memory around
+ * a product (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * checks, launch plans and results as qh_gemm, but the launch scratch (argmax table, stream-K partials and counters)
+ * lives in a static device array of the library (128 MiB + 48.25 KiB per GPU, held until the process ends, set up by
+ * qh_open) instead of the context's allocations; it calls no allocating routine. Products never need more scratch
+ * than that (the launch planner sizes stream-K to it; argmax takes at most 64 logit rows, QH_EINVAL beyond). Calls
+ * that overlap on one GPU share the array and race: serialise them (one stream). */
+int qh_gemm_noalloc(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
+                    const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole);
+
 /* Gemm::put_block (core.rs:619-657): rewrite the 16-row block `block` of an int4 matrix made by qh_mat_quant_rows
  * with stored rows rows16[0..16) of q (zero points `zeros`), counting it as valid. Stages through the matrix's own
  * staging buffer (allocated at upload, like Gemm::block_stage): no allocation. */

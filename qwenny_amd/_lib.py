@@ -56,6 +56,7 @@ SIGNATURES = {
     "qh_mat_split": (I, [P, P, S]),
     "qh_part_len": (S, [P, P, S, S]),
     "qh_gemm": (I, [P, P, P, P, S, S, P, S, P, I, P, I]),
+    "qh_gemm_noalloc": (I, [P, P, P, P, S, S, P, S, P, I, P, I]),
     "qh_put_block": (I, [P, P, P, ctypes.POINTER(QuantC), P, S, P]),
 }
 

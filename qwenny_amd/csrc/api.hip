@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "gemm.h"
 #include "internal.h"
 #include "kernels.h"
 #include "layout.h"
@@ -29,6 +30,8 @@ struct qh_ctx {
     void* sk_scratch;
     int stream_k;
 };
+
+int qh::ctx_device(const qh_ctx* ctx) { return ctx->device; }
 
 static int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
@@ -64,14 +67,14 @@ extern "C" int qh_open(int device, qh_ctx** out) {
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
     // QH_SKINNY_MAX_W / QH_SKINNY_TILE_WAVES override the skinny partition (tuning sweeps)
     void* scratch = nullptr;
-    const size_t scratch_bytes = ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8 + 256;
+    const size_t scratch_bytes = ARGMAX_SCRATCH_BYTES;
     HIP_TRY(hipMalloc(&scratch, scratch_bytes));
     if (hipMemset(scratch, 0, scratch_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         (void)hipFree(scratch);
         return fail(QH_EHIP, "argmax scratch: clear failed");
     }
     void* sk = nullptr;
-    const size_t sk_bytes = PF_SK_PART_BYTES + PF_SK_ITEMS_MAX * sizeof(unsigned);
+    const size_t sk_bytes = PF_SK_SCRATCH_BYTES;
     if (hipMalloc(&sk, sk_bytes) != hipSuccess) {
         (void)hipFree(scratch);
         return fail(QH_ENOMEM, "prefill scratch of %zu bytes: allocation failed", sk_bytes);
@@ -81,6 +84,11 @@ extern "C" int qh_open(int device, qh_ctx** out) {
         (void)hipFree(scratch);
         (void)hipFree(sk);
         return fail(QH_EHIP, "prefill scratch: clear failed");
+    }
+    if (int e = noalloc_init(device)) {
+        (void)hipFree(scratch);
+        (void)hipFree(sk);
+        return e;
     }
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
                       std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
@@ -301,7 +309,8 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
 
 // The launch of a product of m tokens (epi, x, y and keys as qh_gemm takes them; `whole`: one partial).
 static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, size_t ldx, size_t m,
-                          const int32_t* out_rows, void* y, int epi, uint64_t* keys, int whole, void* stream) {
+                          const int32_t* out_rows, void* y, int epi, uint64_t* keys, int whole, void* stream,
+                          const Scratch& sc) {
     Launch l{};
     l.codes = w->codes;
     l.scales = w->scales;
@@ -319,15 +328,15 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
     l.y = y;
     l.ldy = (int)(epi == QH_EPI_SILU ? w->rows / 2 : w->rows);
     l.keys = (unsigned long long*)keys;
-    l.argmax_table = (unsigned long long*)ctx->argmax_scratch;
-    l.argmax_count = (unsigned*)((uint8_t*)ctx->argmax_scratch + ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8);
+    l.argmax_table = (unsigned long long*)sc.argmax;
+    l.argmax_count = (unsigned*)((uint8_t*)sc.argmax + ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8);
     l.epi = epi;
     l.stream = (hipStream_t)stream;
     l.bf16_magic = 0x43004300u;
     l.cus = ctx->cus;
     l.pf_shape = ctx->pf_shape;
-    l.sk_part = (float*)ctx->sk_scratch;
-    l.sk_count = (unsigned*)((uint8_t*)ctx->sk_scratch + PF_SK_PART_BYTES);
+    l.sk_part = (float*)sc.stream_k;
+    l.sk_count = (unsigned*)((uint8_t*)sc.stream_k + PF_SK_PART_BYTES);
     l.stream_k = ctx->stream_k;
     l.nib_mask = 0x000F000Fu;
     l.ks = 1;
@@ -351,7 +360,8 @@ extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
     if (n == 0) return 1;
     if (n <= (size_t)SKINNY_MAX_M) return skinny_partition(ctx, m, n, true).split;
     if (n > (size_t)PF_KS_MAX_M || n > (1u << 24)) return 1;
-    Launch l = make_launch(ctx, m, nullptr, m->cols, n, nullptr, nullptr, QH_EPI_PLAIN, nullptr, 0, nullptr);
+    Launch l = make_launch(ctx, m, nullptr, m->cols, n, nullptr, nullptr, QH_EPI_PLAIN, nullptr, 0, nullptr,
+                           Scratch{ctx->argmax_scratch, ctx->sk_scratch});
     l.dry_run = 1;
     if (hipError_t e = launch(l); e != hipSuccess) return fail(QH_EHIP, "split: %s", hipGetErrorString(e));
     return l.split;
@@ -370,8 +380,10 @@ extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size
     return len;
 }
 
-extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
-                       const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
+// qh_gemm's checks and launch, with the scratch (argmax table and counter, stream-K partials and counters) at `sc`.
+int qh::gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
+                          const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole,
+                          const Scratch& sc) {
     if (!ctx || !w || !x || !y) return fail(QH_EINVAL, "gemm: null");
     if (epi != QH_EPI_PLAIN && epi != QH_EPI_SILU && epi != QH_EPI_ARGMAX) return fail(QH_EINVAL, "epilogue %d", epi);
     if (epi == QH_EPI_ARGMAX && !keys) return fail(QH_EINVAL, "argmax without keys");
@@ -388,10 +400,17 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     // offsets from x
     if (m > (size_t)SKINNY_MAX_M && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
         return fail(QH_EINVAL, "gemm: %zu token rows of %zu elements: x must fit in 4 GiB", n, ldx);
-    Launch l = make_launch(ctx, w, x, ldx, m, out_rows, y, epi, keys, whole, stream);
+    Launch l = make_launch(ctx, w, x, ldx, m, out_rows, y, epi, keys, whole, stream, sc);
     hipError_t e = launch(l);
     if (e != hipSuccess) return fail(QH_EHIP, "gemm launch: %s", hipGetErrorString(e));
     return l.split;
+}
+
+extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
+                       const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
+    if (!ctx) return fail(QH_EINVAL, "gemm: null");
+    return gemm_with_scratch(ctx, stream, w, x, ldx, n, out_rows, n_out, y, epi, keys, whole,
+                             Scratch{ctx->argmax_scratch, ctx->sk_scratch});
 }
 
 extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros,

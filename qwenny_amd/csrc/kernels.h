@@ -91,6 +91,16 @@ size_t skinny_lds(const Launch& l);
 
 enum { EPI_PLAIN = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
 
+// Scratch of a product launch: the argmax table (ARGMAX_SPREAD x ARGMAX_MAX_TOK u64) followed by its workgroup counter
+// (ARGMAX_SCRATCH_BYTES in all), and the stream-K partials (PF_SK_PART_BYTES) followed by PF_SK_ITEMS_MAX item counters
+// (PF_SK_SCRATCH_BYTES in all); every counter and table entry zero between launches.
+struct Scratch {
+    void* argmax;
+    void* stream_k;
+};
+constexpr size_t ARGMAX_SCRATCH_BYTES = (size_t)ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8 + 256;
+constexpr size_t PF_SK_SCRATCH_BYTES = PF_SK_PART_BYTES + PF_SK_ITEMS_MAX * sizeof(unsigned);
+
 // The kernels of one storage format F and epilogue EPI: the skinny kernel for m <= SKINNY_MAX_M, else the prefill
 // kernel.
 template <int F, int EPI>
