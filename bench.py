@@ -38,9 +38,20 @@ def int8_bytes(k, n, m):
 
 
 def quant(seed, kind, k, n):
-    from tests.helpers import make_quant
+    """A synthetic stored matrix [n][k] in the checkpoint's form: 'i4' symmetric int4, 'i4z' int4 with packed zero
+    points, 'i8' per-channel int8, 'i8g' int8 with a scale per row and 128 columns (qwenny_amd.synth)."""
+    from qwenny_amd import synth
+    from qwenny_amd.checkpoint import quant_from_packed
 
-    return make_quant(seed, kind, n, k)
+    name = f"{kind}_{n}_{k}"
+    if kind in ("i8", "i8g"):
+        g = 128 if kind == "i8g" else 0
+        t = synth.int8_quant(seed, name, n, k, group=g)
+        return quant_from_packed(t["weight_packed"], synth.bf16_to_f32(t["weight_scale"]), 8, g, None,
+                                 t["weight_shape"])
+    t = synth.int4_quant(seed, name, n, k, zp=kind == "i4z")
+    return quant_from_packed(t["weight_packed"], synth.bf16_to_f32(t["weight_scale"]), 4, 128,
+                             t.get("weight_zero_point"), t["weight_shape"])
 
 
 def upload_copies(gemm, q, copies):
@@ -102,10 +113,12 @@ class Step:
         return sum(f for *_, f in self.launches)
 
 
-def time_step(step, steps, warmup, graph=True, per_graph=10):
-    """ms per step over `steps` steps, HIP events on the launching stream, after `warmup` steps. With `graph`, the
-    step's launches are captured `per_graph` times into one HIP graph (so that the replay's own start-up, about
-    20 us, is spread over that many steps) and the graph is replayed steps / per_graph times."""
+def time_step(step, steps, warmup, graph=True, per_graph=10, min_reps=100, stats=None):
+    """ms per step: the MEDIAN over at least `min_reps` timed repetitions (whatever `steps` is), each repetition timed
+    with its own pair of HIP events on the launching stream, after `warmup` untimed steps. With `graph`, the step's
+    launches are captured `per_graph` times into one HIP graph (so that a replay's own start-up, about 20 us, is
+    spread over that many steps) and one repetition is one replay; else one repetition is one eager step. `stats`
+    (a dict) receives the mean and the spread of the repetitions and the steps timed."""
     import torch
 
     stream = torch.cuda.current_stream()
@@ -120,20 +133,25 @@ def time_step(step, steps, warmup, graph=True, per_graph=10):
                 for _ in range(per_graph):
                     step.run(s)
         torch.cuda.synchronize()
-        go, reps = g.replay, max(1, steps // per_graph)
+        go = g.replay
         warm = max(1, warmup // per_graph)
     else:
-        go, reps, warm, per_graph = step.run, steps, warmup, 1
+        go, warm, per_graph = step.run, warmup, 1
+    reps = max(min_reps, -(-steps // per_graph))
     for _ in range(warm):
         go()
     torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(reps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for i in range(reps):
         go()
-    t1.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / (reps * per_graph)
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(reps)]) / per_graph
+    if stats is not None:
+        stats.update({"reps": reps, "steps_timed": reps * per_graph, "mean_ms": float(per.mean()),
+                      "p10_ms": float(np.percentile(per, 10)), "p90_ms": float(np.percentile(per, 90))})
+    return float(np.median(per))
 
 
 def cpu_baseline(budget_s=12.0):
@@ -155,6 +173,7 @@ def cpu_baseline(budget_s=12.0):
         if el >= budget_s:
             break
     return {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "host_cpus": os.cpu_count(), "host_cpus_usable": len(os.sched_getaffinity(0)),
             "sample": f"{passes} pass(es) over the 27B decode layer set (5 matrices, 170.5 MB) at M=1, "
                       f"scalar C restatement of Quant::row_into + f32 dot, {threads} threads, {el:.1f} s"}
 
@@ -317,13 +336,13 @@ SET_4B = [(2560, 4096), (4096, 2560), (2560, 1024), (2560, 9728), (2560, 9728), 
 
 
 def set4b_line(gemm, args):
-    """the 4B-scale layer set, int4 with packed zero points, at M = 1 and 8, 12 distinct
+    """the 4B-scale layer set, int4 with packed zero points, at M = 1, 2, 4, 5 and 8, 12 distinct
     device copies (590 MB per pass, beyond the 256 MB MALL), HIP graphs: HBM GB/s over the algorithmic bytes."""
     from qwenny_amd import Epi
 
     mats = [upload_copies(gemm, quant(600 + i, "i4z", k, n), 12) for i, (k, n) in enumerate(SET_4B)]
     out = {}
-    for m in (1, 8):
+    for m in (1, 2, 4, 5, 8):
         st = Step(gemm, m, 9728)
         for c in range(12):
             for ms_, (k, n) in zip(mats, SET_4B):
@@ -396,8 +415,8 @@ def consumers_line(args):
 
 
 class SummedStep(Step):
-    """A Step of one plain product followed by the sum of its split partials (`sum_parts`), so that products that
-    return several partials are timed with the consumer's read of them."""
+    """A Step of one plain product followed, when it returns several partials, by their sum (`sum_parts`): a product
+    of split 1 is already the sum and has no consumer launch."""
 
     def __init__(self, gemm, m, kmax, mat):
         import torch
@@ -410,27 +429,95 @@ class SummedStep(Step):
         from qwenny_amd import sum_parts
 
         super().run(stream)
-        mat, _, y, _, _ = self.launches[0]
-        sum_parts(stream, y, self.split, self.m, mat.rows, self.sum)
+        if self.split > 1:
+            mat, _, y, _, _ = self.launches[0]
+            sum_parts(stream, y, self.split, self.m, mat.rows, self.sum)
 
 
 def short_prefill_line(gemm, set_mats, args):
     """Plain int4 products of 64, 256 and 512 tokens on the 27B prefill shapes (K slices or stream-K, whichever the
-    launcher picks), each with the sum of its partials, in HIP graphs: TFLOP/s of the product and the split used."""
+    launcher picks), in HIP graphs: TFLOP/s of the product alone, and of the product followed by the sum of its
+    partials (sum_parts, only when the split is above 1), with the split used."""
     from qwenny_amd import Epi
 
     out = {}
     for m in (64, 256, 512):
         for i, (k, n) in enumerate(PREFILL_27B):
             mat = set_mats[[0, 2, 3][i]][0]
+            alone = Step(gemm, m, k)
+            alone.add(mat, Epi.Plain, int4_bytes(k, n, m), 2 * m * k * n)
+            ms_a = time_step(alone, max(50, args.steps), 5, not args.no_graph)
             st = SummedStep(gemm, m, k, mat)
             st.add(mat, Epi.Plain, int4_bytes(k, n, m), 2 * m * k * n)
             ms = time_step(st, max(50, args.steps), 5, not args.no_graph)
+            tf_a = alone.flops() / (ms_a * 1e-3) / 1e12
             tf = st.flops() / (ms * 1e-3) / 1e12
-            out[f"m{m}_{k}x{n}"] = {"TFLOPs": round(tf, 1), "split": st.split}
-            print(f"# prefill + sum M={m} K={k} N={n}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s, split {st.split}",
-                  file=sys.stderr, flush=True)
+            out[f"m{m}_{k}x{n}"] = {"TFLOPs": round(tf_a, 1), "TFLOPs_with_sum": round(tf, 1), "split": st.split}
+            print(f"# prefill M={m} K={k} N={n}: {ms_a * 1e3:.1f} us alone ({tf_a:.1f} TFLOP/s), "
+                  f"{ms * 1e3:.1f} us with the sum ({tf:.1f}), split {st.split}", file=sys.stderr, flush=True)
     return {"prefill_short_TFLOPs": out}
+
+
+def config0_line(gemm, args):
+    """BASELINE.json configs[0] on the GPU: the single int4 GEMV M=1, K=2560, N=9728, symmetric, over 48 distinct
+    device copies (617 MB per pass, beyond the 256 MB MALL) in HIP graphs: HBM GB/s over the algorithmic bytes."""
+    from qwenny_amd import Epi
+
+    k, n = 2560, 9728
+    mats = upload_copies(gemm, quant(650, "i4", k, n), 48)
+    st = Step(gemm, 1, k)
+    for m in mats:
+        st.add(m, Epi.Plain, int4_bytes(k, n, 1), 2 * k * n)
+    ms = time_step(st, args.steps, args.warmup, not args.no_graph, per_graph=2)
+    gbs = round(st.bytes() / (ms * 1e-3) / 1e9, 1)
+    print(f"# configs[0] M=1 (2560, 9728): {ms * 1e3 / len(st.launches):.2f} us per launch, {gbs} GB/s",
+          file=sys.stderr, flush=True)
+    return {"config0_m1_GBps": gbs}
+
+
+def grouped_int8_line(gemm, args):
+    """int8 with a scale per row and 128 columns (the reference's default load mode: bf16 weights requantized at
+    load), on the configs[4] shapes: M = 1 over 4 device copies of (5120, 17408) and (17408, 5120) (GB/s over
+    K N + (K / 128) N 4 + 2 M K + 2 M N), and M = 2048 per shape (TFLOP/s)."""
+    from qwenny_amd import Epi
+
+    shapes = [(5120, 17408), (17408, 5120)]
+    mats = [upload_copies(gemm, quant(660 + i, "i8g", k, n), 4) for i, (k, n) in enumerate(shapes)]
+    gbytes = lambda k, n, m: k * n + (k // 128) * n * 4 + 2 * m * k + 2 * m * n
+    st = Step(gemm, 1, 17408)
+    for c in range(4):
+        for ms_, (k, n) in zip(mats, shapes):
+            st.add(ms_[c], Epi.Plain, gbytes(k, n, 1), 2 * k * n)
+    ms1 = time_step(st, args.steps, args.warmup, not args.no_graph)
+    out = {"m1_GBps": round(st.bytes() / (ms1 * 1e-3) / 1e9, 1)}
+    for ms_, (k, n) in zip(mats, shapes):
+        stp = Step(gemm, 2048, k)
+        stp.add(ms_[0], Epi.Plain, gbytes(k, n, 2048), 2 * 2048 * k * n)
+        msp = time_step(stp, max(10, args.steps // 10), 3, False)
+        out[f"m2048_{k}x{n}_TFLOPs"] = round(stp.flops() / (msp * 1e-3) / 1e12, 1)
+    print(f"# grouped int8: {out}", file=sys.stderr, flush=True)
+    return {"int8_grouped": out}
+
+
+def prefill_zp_line(gemm, args):
+    """BASELINE.json configs[3] with zero points: int4 with packed zero points, M = 2048, the three 27B prefill
+    shapes, activations with 1% outlier columns x20 (TFLOP/s)."""
+    import torch
+
+    from qwenny_amd import Epi
+    from qwenny_amd.synth import activations
+
+    out = {}
+    for i, (k, n) in enumerate(PREFILL_27B):
+        mat = upload_copies(gemm, quant(670 + i, "i4z", k, n), 1)[0]
+        st = Step(gemm, 2048, k)
+        st.x = torch.from_numpy(activations(671, "x", 2048, k, outliers=0.01).view(np.int16)).cuda().view(
+            torch.bfloat16)
+        st.add(mat, Epi.Plain, int4_bytes(k, n, 2048, zp=True), 2 * 2048 * k * n)
+        msp = time_step(st, max(10, args.steps // 10), 3, False)
+        out[f"{k}x{n}"] = round(st.flops() / (msp * 1e-3) / 1e12, 1)
+    print(f"# prefill M=2048 with zero points: {out} TFLOP/s", file=sys.stderr, flush=True)
+    return {"prefill_zp_m2048_TFLOPs": out}
 
 
 def summarize_clock(pmc_dir, min_ns=50000):
@@ -470,10 +557,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of lines: m1,m5,prefill,pfshort,int8,dense,dequant,set4b,consumers")
+    ap.add_argument("--only", default="",
+                    help="comma list of lines: m1,m5,prefill,pfzp,pfshort,int8,i8g,dense,dequant,set4b,c0,consumers")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
+    ap.add_argument("--set4b-run", action="store_true",
+                    help="the profiling workload of configs[1]: the 4B layer set at M=1, with zero points and "
+                         "symmetric, 5 eager launches per matrix each")
     ap.add_argument("--prefill-run", action="store_true",
                     help="the prefill profiling workload: 5 launches of each M=2048 prefill shape, no graph")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -500,7 +591,18 @@ def main():
 
     torch.cuda.init()
     gemm = Gemm.load(0)
-    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "pfshort", "int8", "dense", "dequant", "set4b", "consumers"}
+    if args.set4b_run:
+        for kind in ("i4z", "i4"):
+            for i, (k, n) in enumerate(SET_4B):
+                st = Step(gemm, 1, k)
+                st.add(upload_copies(gemm, quant(600 + i, kind, k, n), 1)[0], Epi.Plain, 0, 0)
+                for _ in range(5):
+                    st.run()
+        torch.cuda.synchronize()
+        print(json.dumps({"set4b_run": "done"}))
+        return
+    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "pfzp", "pfshort", "int8", "i8g", "dense",
+                                                         "dequant", "set4b", "c0", "consumers"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
@@ -532,7 +634,8 @@ def main():
 
     out = {}
     step = decode_step(1)
-    ms = time_step(step, args.steps, args.warmup, not args.no_graph)
+    head_stats = {}
+    ms = time_step(step, args.steps, args.warmup, not args.no_graph, stats=head_stats)
     gbs = step.bytes() / (ms * 1e-3) / 1e9
     launches = len(step.launches)
     out["m1"] = {"ms_per_step": ms, "GB/s": gbs, "launches": launches, "bytes": step.bytes()}
@@ -604,6 +707,12 @@ def main():
         extra.update(set4b_line(gemm, args))
     if "consumers" in only:
         extra.update(consumers_line(args))
+    if "c0" in only:
+        extra.update(config0_line(gemm, args))
+    if "i8g" in only:
+        extra.update(grouped_int8_line(gemm, args))
+    if "pfzp" in only:
+        extra.update(prefill_zp_line(gemm, args))
 
     line = {
         "metric": "int4 GEMM HBM GB/s (% of 8 TB/s) at M=1/5; TFLOP/s (% bf16 MFMA peak) at M=2048",
@@ -613,6 +722,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "timing": dict(head_stats, statistic="median of per-replay HIP-event times (10 steps per graph replay)"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -229,10 +229,11 @@ int qh_add_rmsnorm(void* stream, float* h, const float* x, int splits, size_t n,
  * s_t * B (A x) to a plain product for the tokens t whose slot uses it (s_t = slot_scale[tok_slot[t]]; 0: nothing
  * added). xa: the stacked A product's partials f32 [split][n][m_cols] (m_cols <= 256); b_f16: B f16 [rows][rank] in
  * the product's row order (rank 8, 16, 32 or 64; 16-byte aligned); tab: 8 int32, each module's end row (ascending;
- * unused INT_MAX), then its first column of xa (-1: not adapted). All pointers are device addresses.
+ * unused INT_MAX), then its first column of xa (-1: not adapted; a column range must lie within m_cols). rows: a
+ * multiple of 16 (the products' row count). All pointers are device addresses. The delta is computed in f32.
  * lora_add: y [n][ldy] f32, the plain product's split 0, row o += s_t * B[o] . xa[t][off(o) ..].
  * lora_silu: y [n][ldy] f32, a plain [gate; up] product packed in row_order(rows, 1) (split 1), read; mid [n][rows / 2]
- * bf16 = silu(gate + delta) * (up + delta) for every token t < n, as the SwiGLU epilogue writes it (rows % 16 == 0).
+ * bf16 = silu(gate + delta) * (up + delta) for every token t < n, as the SwiGLU epilogue writes it.
  * Launch only. */
 int qh_lora_add(void* stream, const float* xa, int split, int m_cols, const uint16_t* b_f16, int rank, size_t rows,
                 const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n, float* y, size_t ldy);

@@ -1,11 +1,12 @@
 // Consumers of the plain products' split-K partials (the output contract y [split][n][ld] f32): the reference's
 // sum_parts (kernels/qwen.cu:141-143, part_sum kernels/common.cuh:66-70) and add_rmsnorm (kernels/qwen.cu:57-80),
 // the residual step after the o_proj / out_proj / down products, and the LoRA epilogue (kernels/lora.cuh) that adds an
-// unmerged adapter's delta to them. HBM-bound; f32 sums in the reference's order (h + x[0], then x[1], x[2], ..), so
-// the sums are bit-identical to it.
+// unmerged adapter's delta to them. The sums are HBM-bound, in f32 in the reference's order (h + x[0], then x[1], x[2],
+// ..), so they are bit-identical to it; the LoRA delta runs on the f32 matrix cores.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "internal.h"
 
@@ -117,21 +118,42 @@ __global__ __launch_bounds__(T) void add_rmsnorm_kernel(float* __restrict__ h, c
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// LoRA consumers (kernels/lora.cuh:52-113, launched by src/cuda/qwen/lora.rs:143-190): an unmerged adapter adds
-// s_t B (A x) to a plain product for the tokens t of the slots that use it. A x arrives as the split-K partials xa
-// [split][n][M] of the stacked A product (M = adapted modules x rank, at most 256 columns); B is f16 [rows][R] in the
-// product's row order; tab (8 ints) holds each module's end row (ascending; unused INT_MAX), then its first column of
-// xa (-1: not adapted). A workgroup takes LORA_TT tokens and 256 rows (add) or 256 SwiGLU outputs (silu): the tokens'
-// scales and their xa (the partials summed in split order) are staged in LDS once, each thread reads its B row as
-// 16-byte loads and dots it with the staged xa in f32, in column order.
+// LoRA consumers (the reference's lora_add / lora_silu, kernels/lora.cuh:52-113, launched by
+// src/cuda/qwen/lora.rs:143-190): an unmerged adapter adds s_t B (A x) to a plain product for the tokens t of the slots
+// that use it. A x arrives as the split-K partials xa [split][n][cols] of the stacked A product (cols = adapted modules
+// x rank); B is f16 [rows][R] in the product's row order; tab (8 ints) holds each module's end row (ascending; unused
+// INT_MAX), then its first column of xa (-1: not adapted). Kept from the reference: this interface and its meaning.
+//
+// The delta of a 16-row tile for 16 tokens is a rank-R update D = Xs . B^T, done on the f32 matrix cores
+// (v_mfma_f32_16x16x4_f32: full f32 products and sums, R / 4 steps): A operand = the tokens' xa columns scaled by
+// s_t (staged in LDS, summed over the splits once per workgroup), B operand = the tile's B rows (f16, exact in f32).
+// The contraction index is laid out so that each lane reads its B values as one contiguous run of R / 4 halves: lane
+// group q = lane / 16 takes k = q R / 4 + i for step i. Module routing is per tile: a tile whose rows lie in one
+// module (every tile, when module ends are multiples of 16) takes one pass; a tile that straddles a module end takes
+// one pass per module with the other modules' B rows masked to zero. The D layout is the one the decode product's
+// accumulators have: lane l holds D[token 4 (l / 16) + i][row l % 16], i = 0..3.
+//
+// A workgroup takes WT * 64 rows (LORA_WAVES waves of WT tiles each: 4 for 17 tokens and more, 1 for fewer, where the
+// launch would otherwise have too few waves) and up to LORA_TOK tokens (one 16-token block: at most 33 KiB of LDS, so
+// that several workgroups per CU hide each other's memory round trips). The deltas go through LDS so that y is read and written along its rows (whole
+// cache lines), not in the MFMA's 16-row pieces.
 
-constexpr int LORA_TT = 8;
-constexpr int LORA_MAXM = 256;
+constexpr int LORA_COLS_MAX = 256;  // columns of xa at most (four modules of rank 64)
+constexpr int LORA_TOK = 16;        // tokens per workgroup at most (one 16-token block)
+constexpr int LORA_WAVES = 4;
+// LDS row pitches (floats): off a multiple of the 64 banks, so that the 16 lanes reading 16 token rows of xs (or the
+// lane groups writing 4 token rows of the deltas) hit distinct banks
+constexpr int LORA_XS_LD = LORA_COLS_MAX + 1;
+template <int WT>
+constexpr int lora_dl_ld() { return WT * 64 + 4; }
+
+typedef float lf32x4 __attribute__((ext_vector_type(4)));
 
 struct LoraArgs {
     const float* xa;
-    int split, M;
+    int split, cols;
     const uint16_t* b;
+    int rank;
     int rows;
     const int* tab;
     const int* tok_slot;
@@ -140,131 +162,224 @@ struct LoraArgs {
     int ldy;
 };
 
-// the block's token scales (0 past n) and, for the tokens with a nonzero scale, xa summed over the splits
-__device__ void lora_stage(const LoraArgs& a, int t0, float (*xs)[LORA_MAXM], float* sc) {
-    if (threadIdx.x < LORA_TT) {
+// module of output row o: how many module ends lie at or below it
+__device__ __forceinline__ int lora_module(const int* tab, int o) {
+    int m = 0;
+#pragma unroll
+    for (int i = 0; i < 3; i++) m += o >= tab[i];
+    return m;
+}
+
+// xs[t][c] = s_t * sum over splits of xa[.][t0 + t][c] for the workgroup's tokens (0 without the adapter),
+// sc[t] = s_t (0 past n). Every thread's xa loads are issued at once, before the slot scales are known (they only
+// multiply the sums): one memory round trip beside the scales' two.
+__device__ void lora_stage_xs(const LoraArgs& a, int t0, float* xs, float* sc) {
+    constexpr int PER = LORA_TOK * LORA_COLS_MAX / (64 * LORA_WAVES);  // elements per thread at most
+    const int tn = min(LORA_TOK, a.n - t0), ne = tn * a.cols;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) v[k] = 0.0f;
+    for (int s = 0; s < a.split; s++) {
+        const float* xp = a.xa + ((size_t)s * a.n + t0) * a.cols;  // [tn][cols] contiguous
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int i = threadIdx.x + k * 64 * LORA_WAVES;
+            if (i < ne) v[k] += xp[i];
+        }
+    }
+    if (threadIdx.x < LORA_TOK) {
         const int t = t0 + threadIdx.x;
         sc[threadIdx.x] = t < a.n ? a.slot_scale[a.tok_slot[t]] : 0.0f;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < LORA_TT * a.M; i += blockDim.x) {
-        const int tl = i / a.M, c = i - tl * a.M, t = t0 + tl;
-        float v = 0.0f;
-        if (sc[tl] != 0.0f)
-            for (int s = 0; s < a.split; s++) v += a.xa[((size_t)s * a.n + t) * a.M + c];
-        xs[tl][c] = v;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = threadIdx.x + k * 64 * LORA_WAVES;
+        if (i < ne) {
+            const int t = i / a.cols, c = i - t * a.cols;
+            xs[t * LORA_XS_LD + c] = sc[t] != 0.0f ? v[k] * sc[t] : 0.0f;
+        }
     }
     __syncthreads();
 }
 
-// B row o (f16 [R]) as f32
+// The lane's raw B words for row o, columns q R / 4 .. + R / 4 (f16 pairs)
 template <int R>
-__device__ __forceinline__ void lora_b_row(const uint16_t* b, int o, float (&w)[R]) {
-    const uint4* p = (const uint4*)(b + (size_t)o * R);
+__device__ __forceinline__ void lora_b_load(const uint16_t* b, int o, uint32_t (&w)[R / 8]) {
+    const int q = (threadIdx.x & 63) >> 4;
+    const uint16_t* p = b + (size_t)o * R + q * (R / 4);
+    if constexpr (R / 4 >= 8) {
 #pragma unroll
-    for (int i = 0; i < R / 8; i++) {
-        const uint4 u = p[i];
-        const uint32_t h[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            w[8 * i + 2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h[k] & 0xffffu));
-            w[8 * i + 2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h[k] >> 16));
+        for (int i = 0; i < R / 8; i += 4) {
+            const uint4 u = *(const uint4*)(p + 2 * i);
+            w[i] = u.x, w[i + 1] = u.y, w[i + 2] = u.z, w[i + 3] = u.w;
         }
+    } else if constexpr (R / 4 == 4) {
+        const uint2 u = *(const uint2*)p;
+        w[0] = u.x, w[1] = u.y;
+    } else {
+        w[0] = *(const uint32_t*)p;
     }
 }
 
-template <int R>
-__device__ __forceinline__ float lora_dot(const float (&w)[R], const float* x) {
-    float d = 0.0f;
-#pragma unroll
-    for (int j = 0; j < R; j++) d = __builtin_fmaf(w[j], x[j], d);
-    return d;
-}
+// The workgroup's part of a LoRA launch: B words of the wave's tiles and the workgroup's y values are loaded first (in
+// flight while the tokens' xa is staged), then the deltas of each tile (one masked MFMA pass per module present,
+// module_of(row) and off[module]) go through LDS to the threads that own y's rows.
+template <int R, int WT>
+struct LoraTiles {
+    static constexpr int DL_LD = lora_dl_ld<WT>();
+    uint32_t bw[WT][R / 8];
 
-// y [n][ldy] (a plain product's split 0) row o += s_t B[o] . xa[t][off(o) ..] for the adapter tokens
-template <int R>
-__global__ __launch_bounds__(256) void lora_add_kernel(LoraArgs a, float* __restrict__ y) {
-    __shared__ float xs[LORA_TT][LORA_MAXM];
-    __shared__ float sc[LORA_TT];
-    const int t0 = blockIdx.y * LORA_TT;
-    lora_stage(a, t0, xs, sc);
-    bool any = false;
+    __device__ void load(const LoraArgs& a, int o0) {
+        const int wave = threadIdx.x >> 6, l16 = threadIdx.x & 15;
 #pragma unroll
-    for (int i = 0; i < LORA_TT; i++) any |= sc[i] != 0.0f;
-    const int o = blockIdx.x * 256 + threadIdx.x;
-    if (!any || o >= a.rows) return;
-    const int mod = (o >= a.tab[0]) + (o >= a.tab[1]) + (o >= a.tab[2]), off = a.tab[4 + mod];
-    if (off < 0) return;
-    float w[R];
-    lora_b_row<R>(a.b, o, w);
-#pragma unroll
-    for (int tl = 0; tl < LORA_TT; tl++)
-        if (sc[tl] != 0.0f) {
-            float* yo = y + (size_t)(t0 + tl) * a.ldy + o;
-            *yo = __builtin_fmaf(sc[tl], lora_dot<R>(w, &xs[tl][off]), *yo);
+        for (int wt = 0; wt < WT; wt++) {
+            const int o = min(o0 + (wave * WT + wt) * 16 + l16, a.rows - 1);
+            lora_b_load<R>(a.b, o, bw[wt]);
         }
+    }
+
+    template <class ModuleOf>
+    __device__ void deltas(const LoraArgs& a, int o0, int tn, const float* xs, const int* off, ModuleOf module_of,
+                           float* dl) const {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int wt = 0; wt < WT; wt++) {
+            const int r0 = (wave * WT + wt) * 16;  // tile's first row in the workgroup
+            if (o0 + r0 >= a.rows) break;               // wave-uniform
+            const int mod = module_of(o0 + r0 + l16), mlo = module_of(o0 + r0), mhi = module_of(o0 + r0 + 15);
+            float bv[R / 4];
+#pragma unroll
+            for (int i = 0; i < R / 8; i++) {
+                bv[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[wt][i] & 0xffffu));
+                bv[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[wt][i] >> 16));
+            }
+            lf32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int m = mlo; m <= mhi; m++) {
+                const int c0 = off[m];
+                if (c0 < 0) continue;  // wave-uniform: module not adapted
+                const bool mine = mod == m;
+                const float* xr = xs + l16 * LORA_XS_LD + c0 + q * (R / 4);
+#pragma unroll
+                for (int i = 0; i < R / 4; i++)
+                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(xr[i], mine ? bv[i] : 0.0f, d, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) dl[(4 * q + i) * DL_LD + r0 + l16] = d[i];
+        }
+        (void)tn;
+        __syncthreads();
+    }
+};
+
+// y [n][ldy] (a plain product's split 0) row o += delta for the adapter tokens; rows of unadapted modules and tokens
+// without the adapter are left as they are. Thread i owns row o0 + i % ROWS of tokens i / ROWS + (256 / ROWS) k.
+template <int R, int WT>
+__global__ __launch_bounds__(64 * LORA_WAVES) void lora_add_kernel(LoraArgs a, float* __restrict__ y) {
+    constexpr int ROWS = WT * 64, DL_LD = lora_dl_ld<WT>(), TS = 64 * LORA_WAVES / ROWS, TPT = LORA_TOK / TS;
+    __shared__ float xs[LORA_TOK * LORA_XS_LD];
+    __shared__ float dl[LORA_TOK * DL_LD];
+    __shared__ float sc[LORA_TOK];
+    const int t0 = blockIdx.y * LORA_TOK, o0 = blockIdx.x * ROWS;
+    const int tn = min(LORA_TOK, a.n - t0);
+    const int c = threadIdx.x % ROWS, tp = threadIdx.x / ROWS, o = min(o0 + c, a.rows - 1);
+    LoraTiles<R, WT> tiles;
+    tiles.load(a, o0);
+    float v[TPT];
+    float* yc = y + (size_t)t0 * a.ldy + o;
+#pragma unroll
+    for (int k = 0; k < TPT; k++) {
+        const int t = tp + TS * k;
+        v[k] = t < tn ? yc[(size_t)t * a.ldy] : 0.0f;
+    }
+    lora_stage_xs(a, t0, xs, sc);
+    const int off[4] = {a.tab[4], a.tab[5], a.tab[6], a.tab[7]};
+    tiles.deltas(a, o0, tn, xs, off, [&](int r) { return lora_module(a.tab, r); }, dl);
+    if (o0 + c >= a.rows || off[lora_module(a.tab, o)] < 0) return;
+#pragma unroll
+    for (int k = 0; k < TPT; k++) {
+        const int t = tp + TS * k;
+        if (t < tn && sc[t] != 0.0f) yc[(size_t)t * a.ldy] = v[k] + dl[t * DL_LD + c];
+    }
 }
 
 // mid [n][rows / 2] (bf16) = SwiGLU of the plain [gate; up] product y [n][ldy] (split 1, packed in the SwiGLU
-// epilogue's row order: 16-row tile p holds gate rows 8p .. 8p + 7, then their up rows) with the delta added first
-template <int R>
-__global__ __launch_bounds__(256) void lora_silu_kernel(LoraArgs a, const float* __restrict__ y, __bf16* mid) {
-    __shared__ float xs[LORA_TT][LORA_MAXM];
-    __shared__ float sc[LORA_TT];
-    const int t0 = blockIdx.y * LORA_TT;
-    lora_stage(a, t0, xs, sc);
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= a.rows / 2) return;
-    const int og = 16 * (j / 8) + j % 8, ou = og + 8, offg = a.tab[4], offu = a.tab[5];
-    float wg[R], wu[R];
-    if (offg >= 0) lora_b_row<R>(a.b, og, wg);
-    if (offu >= 0) lora_b_row<R>(a.b, ou, wu);
-    for (int tl = 0; tl < LORA_TT && t0 + tl < a.n; tl++) {
-        const size_t r = (size_t)(t0 + tl) * a.ldy;
-        float g = y[r + og], u = y[r + ou];
-        if (sc[tl] != 0.0f) {
-            if (offg >= 0) g = __builtin_fmaf(sc[tl], lora_dot<R>(wg, &xs[tl][offg]), g);
-            if (offu >= 0) u = __builtin_fmaf(sc[tl], lora_dot<R>(wu, &xs[tl][offu]), u);
-        }
-        mid[(size_t)(t0 + tl) * (a.rows / 2) + j] = (__bf16)(g / (1.0f + __expf(-g)) * u);
+// epilogue's row order: 16-row tile p holds gate rows 8p .. 8p + 7, then their up rows) with the delta added first:
+// in a tile, rows 0..7 are module 0 (gate, columns from tab[4]) and rows 8..15 module 1 (up, tab[5]). Thread i owns
+// output j = i % (ROWS / 2) of the workgroup's (gate row 16 (j / 8) + j % 8, up row + 8) for tokens
+// i / (ROWS / 2) + TS k.
+template <int R, int WT>
+__global__ __launch_bounds__(64 * LORA_WAVES) void lora_silu_kernel(LoraArgs a, const float* __restrict__ y,
+                                                                   __bf16* __restrict__ mid) {
+    constexpr int ROWS = WT * 64, DL_LD = lora_dl_ld<WT>(), TS = 64 * LORA_WAVES / (ROWS / 2), TPT = LORA_TOK / TS;
+    __shared__ float xs[LORA_TOK * LORA_XS_LD];
+    __shared__ float dl[LORA_TOK * DL_LD];
+    __shared__ float sc[LORA_TOK];
+    const int t0 = blockIdx.y * LORA_TOK, o0 = blockIdx.x * ROWS;
+    const int tn = min(LORA_TOK, a.n - t0);
+    const int half = a.rows / 2, j = threadIdx.x % (ROWS / 2), tp = threadIdx.x / (ROWS / 2);
+    const int rg = 16 * (j >> 3) + (j & 7), og = o0 + rg < a.rows ? o0 + rg : a.rows - 16;  // in bounds
+    LoraTiles<R, WT> tiles;
+    tiles.load(a, o0);
+    float g[TPT], u[TPT];
+#pragma unroll
+    for (int k = 0; k < TPT; k++) {
+        const int t = tp + TS * k;
+        const float* yr = y + (size_t)(t0 + min(t, tn - 1)) * a.ldy + og;
+        g[k] = yr[0];
+        u[k] = yr[8];
+    }
+    lora_stage_xs(a, t0, xs, sc);
+    const int off[2] = {a.tab[4], a.tab[5]};
+    tiles.deltas(a, o0, tn, xs, off, [](int r) { return (r >> 3) & 1; }, dl);
+    if (o0 + rg >= a.rows) return;
+#pragma unroll
+    for (int k = 0; k < TPT; k++) {
+        const int t = tp + TS * k;
+        if (t >= tn) break;
+        const float gg = g[k] + dl[t * DL_LD + rg], uu = u[k] + dl[t * DL_LD + rg + 8];
+        mid[(size_t)(t0 + t) * half + o0 / 2 + j] = (__bf16)(gg / (1.0f + __expf(-gg)) * uu);
     }
 }
 
-int lora_launch(void* stream, const LoraArgs& a, int rank, float* y_add, const float* y_silu, __bf16* mid) {
+int lora_launch(void* stream, const LoraArgs& a, float* y_add, const float* y_silu, __bf16* mid) {
     const bool silu = mid != nullptr;
-    const unsigned per = 256, outs = (unsigned)(silu ? a.rows / 2 : a.rows);
-    const dim3 grid((outs + per - 1) / per, (unsigned)((a.n + LORA_TT - 1) / LORA_TT));
     hipStream_t s = (hipStream_t)stream;
-#define QH_LORA_CASE(R)                                                                      \
-    case R:                                                                                  \
-        if (silu)                                                                            \
-            hipLaunchKernelGGL(lora_silu_kernel<R>, grid, dim3(256), 0, s, a, y_silu, mid);  \
-        else                                                                                 \
-            hipLaunchKernelGGL(lora_add_kernel<R>, grid, dim3(256), 0, s, a, y_add);         \
-        break;
-    switch (rank) {
-        QH_LORA_CASE(8)
-        QH_LORA_CASE(16)
-        QH_LORA_CASE(32)
-        QH_LORA_CASE(64)
-        default: return fail(QH_EINVAL, "LoRA rank %d: ranks 8, 16, 32 and 64 are served", rank);
-    }
-#undef QH_LORA_CASE
+    auto go = [&](auto rank, auto wt) {
+        constexpr int R = decltype(rank)::value, WT = decltype(wt)::value;
+        const dim3 grid((unsigned)((a.rows + WT * 64 - 1) / (WT * 64)), (unsigned)((a.n + LORA_TOK - 1) / LORA_TOK));
+        if (silu)
+            hipLaunchKernelGGL((lora_silu_kernel<R, WT>), grid, dim3(64 * LORA_WAVES), 0, s, a, y_silu, mid);
+        else
+            hipLaunchKernelGGL((lora_add_kernel<R, WT>), grid, dim3(64 * LORA_WAVES), 0, s, a, y_add);
+    };
+    auto by_rank = [&](auto wt) -> bool {
+        switch (a.rank) {
+            case 8: go(std::integral_constant<int, 8>{}, wt); return true;
+            case 16: go(std::integral_constant<int, 16>{}, wt); return true;
+            case 32: go(std::integral_constant<int, 32>{}, wt); return true;
+            case 64: go(std::integral_constant<int, 64>{}, wt); return true;
+            default: return false;
+        }
+    };
+    // decode-sized steps: one tile per wave (4x the workgroups of a launch that would otherwise leave most CUs idle)
+    const bool ok = a.n <= LORA_TOK ? by_rank(std::integral_constant<int, 1>{}) : by_rank(std::integral_constant<int, 4>{});
+    if (!ok) return fail(QH_EINVAL, "LoRA rank %d: ranks 8, 16, 32 and 64 are served", a.rank);
     if (hipError_t e = hipGetLastError(); e != hipSuccess)
         return fail(QH_EHIP, "lora launch: %s", hipGetErrorString(e));
     return QH_OK;
 }
 
 int lora_check(const float* xa, int split, int m_cols, const uint16_t* b, size_t rows, const int32_t* tab,
-               const int32_t* tok_slot, const float* slot_scale, size_t n, const void* y, size_t ldy, bool silu) {
+               const int32_t* tok_slot, const float* slot_scale, size_t n, const void* y, size_t ldy) {
     if (!xa || !b || !tab || !tok_slot || !slot_scale || !y || split < 1)
         return fail(QH_EINVAL, "lora: null or %d splits", split);
-    if (m_cols < 1 || m_cols > LORA_MAXM)
-        return fail(QH_EINVAL, "lora: %d columns of xa (at most %d)", m_cols, LORA_MAXM);
-    if (rows == 0 || rows > (1u << 30) || n > (1u << 24) || ldy < rows || ldy > (1u << 30) || (uintptr_t)b % 16 ||
-        (silu && rows % 16))
-        return fail(QH_EINVAL, "lora: %zu rows (ld %zu), %zu tokens, B 16-byte aligned%s", rows, ldy, n,
-                    silu ? ", rows a multiple of 16" : "");
+    if (m_cols < 1 || m_cols > LORA_COLS_MAX)
+        return fail(QH_EINVAL, "lora: %d columns of xa (at most %d)", m_cols, LORA_COLS_MAX);
+    if (rows == 0 || rows % 16 || rows > (1u << 30) || n > (1u << 24) || ldy < rows || ldy > (1u << 30) ||
+        (uintptr_t)b % 16)
+        return fail(QH_EINVAL, "lora: %zu rows (ld %zu), %zu tokens: rows a multiple of 16, B 16-byte aligned", rows,
+                    ldy, n);
     return QH_OK;
 }
 
@@ -274,9 +389,9 @@ extern "C" int qh_lora_add(void* stream, const float* xa, int split, int m_cols,
                            size_t rows, const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n,
                            float* y, size_t ldy) {
     if (n == 0) return QH_OK;
-    if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy, false)) return e;
-    const LoraArgs a{xa, split, m_cols, b_f16, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
-    return lora_launch(stream, a, rank, y, nullptr, nullptr);
+    if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy)) return e;
+    const LoraArgs a{xa, split, m_cols, b_f16, rank, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
+    return lora_launch(stream, a, y, nullptr, nullptr);
 }
 
 extern "C" int qh_lora_silu(void* stream, const float* xa, int split, int m_cols, const uint16_t* b_f16, int rank,
@@ -284,9 +399,9 @@ extern "C" int qh_lora_silu(void* stream, const float* xa, int split, int m_cols
                             size_t n, const float* y, size_t ldy, void* mid_bf16) {
     if (n == 0) return QH_OK;
     if (!mid_bf16) return fail(QH_EINVAL, "lora silu: null output");
-    if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy, true)) return e;
-    const LoraArgs a{xa, split, m_cols, b_f16, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
-    return lora_launch(stream, a, rank, nullptr, y, (__bf16*)mid_bf16);
+    if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy)) return e;
+    const LoraArgs a{xa, split, m_cols, b_f16, rank, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
+    return lora_launch(stream, a, nullptr, y, (__bf16*)mid_bf16);
 }
 
 // launch sum_parts_kernel over n4 float4: workgroups of 64 threads for decode-sized rows (one float4 per thread over

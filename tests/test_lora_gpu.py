@@ -33,17 +33,22 @@ def _b16(b):
     return _dev(np.ascontiguousarray(b, np.float16).view(np.int16), torch.int16)
 
 
-@pytest.mark.parametrize("rank,split,n,m_cols", [(8, 1, 1, 16), (16, 3, 5, 48), (32, 2, 13, 96), (64, 4, 17, 256)])
-def test_lora_add_matches_oracle(gemm, rank, split, n, m_cols):
+@pytest.mark.parametrize("rank,split,n,m_cols,ends", [
+    (8, 1, 1, 16, (64, 128)), (16, 3, 5, 48, (64, 128)), (32, 2, 13, 96, (64, 128)), (64, 4, 17, 256, (64, 128)),
+    (16, 2, 40, 48, (72, 130)), (64, 1, 33, 256, (8, 184))])
+def test_lora_add_matches_oracle(gemm, rank, split, n, m_cols, ends):
+    """Module ends on tile boundaries (64, 128) and inside tiles (72, 130; 8, 184): a tile that straddles a module end
+    takes each module's rows with that module's columns of xa; 33 and 40 tokens span two token workgroups."""
     import torch
 
-    print(f"lora_add rank={rank} split={split} n={n}", flush=True)
+    print(f"lora_add rank={rank} split={split} n={n} ends={ends}", flush=True)
     rng = np.random.default_rng(rank * 100 + n)
     rows = 192
     xa = rng.standard_normal((split, n, m_cols)).astype(np.float32)
     b = (rng.standard_normal((rows, rank)) * 0.1).astype(np.float16)
-    # three modules: rows 0..63 from column 0, 64..127 not adapted, 128..191 from the last rank columns
-    tab = np.array([64, 128, INT_MAX, INT_MAX, 0, -1, m_cols - rank, -1], np.int32)
+    # three modules: rows 0..e0 from column 0, e0..e1 not adapted, e1..191 from the last rank columns
+    e0, e1 = ends
+    tab = np.array([e0, e1, INT_MAX, INT_MAX, 0, -1, m_cols - rank, -1], np.int32)
     slot_scale = np.array([0.0, 0.25, 2.0], np.float32)
     tok_slot = rng.integers(0, 3, n).astype(np.int32)
     y0 = rng.standard_normal((n, rows)).astype(np.float32)
@@ -55,7 +60,7 @@ def test_lora_add_matches_oracle(gemm, rank, split, n, m_cols):
     assert rel_err(got, want) <= 1e-5
     untouched = slot_scale[tok_slot] == 0
     assert (got[untouched] == y0[untouched]).all()
-    assert (got[:, 64:128] == y0[:, 64:128]).all()
+    assert (got[:, e0:e1] == y0[:, e0:e1]).all()
 
 
 @pytest.mark.parametrize("m", [1, 5, 40, 64, 200])
