@@ -458,6 +458,70 @@ def short_prefill_line(gemm, set_mats, args):
     return {"prefill_short_TFLOPs": out}
 
 
+def lora_line(gemm, args):
+    """An unmerged rank-16 LoRA adapter on the 27B [gate; up] (34816 x 5120, SwiGLU) and down (5120 x 17408, plain)
+    products at M = 1 and 2048, HIP graphs: the adapter fused into the product's epilogue (qh_gemm_lora) against the
+    reference's sequence (the plain product, then lora_silu over its f32 [gate; up] output, or lora_add on its split
+    0), with the product without adapter beside them; microseconds per product."""
+    import torch
+
+    from qwenny_amd import Epi, lora_add, lora_silu
+
+    rank = 16
+    gu = upload_copies(gemm, quant(690, "i4", 5120, 34816), 4)
+    dn = upload_copies(gemm, quant(691, "i4", 17408, 5120), 4)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    out = {}
+    for m, copies in ((1, 4), (2048, 1)):
+        xg = torch.randn(m, 17408, device="cuda").to(torch.bfloat16)
+        res = {}
+        for name, mats, rows, k in (("gate_up_silu", gu, 34816, 5120), ("down_plain", dn, 5120, 17408)):
+            silu = name.startswith("gate")
+            cols = 2 * rank
+            xa = torch.randn(1, m, cols, device="cuda", generator=g)
+            b = (torch.randn(rows, rank, device="cuda", generator=g) * 0.05).half().view(torch.int16)
+            tab = torch.tensor([2**31 - 1] * 4 + [0, rank if silu else -1, -1, -1], dtype=torch.int32, device="cuda")
+            slot = torch.zeros(m, dtype=torch.int32, device="cuda")
+            scale = torch.tensor([1.0], dtype=torch.float32, device="cuda")
+            lora = (xa, 1, cols, b, rank, tab, slot, scale)
+            split = mats[0].split(m)
+            yf = torch.empty(split * m * rows, dtype=torch.float32, device="cuda")
+            mid = torch.empty(m * rows // 2, dtype=torch.bfloat16, device="cuda")
+            use = mats[:copies]
+
+            class Fused(Step):
+                def run(self, stream=None):
+                    for mt in use:
+                        gemm.run_lora(stream, m, mt, xg, mid if silu else yf, Epi.Silu if silu else Epi.Plain, lora,
+                                      ldx=17408)
+
+            class Unfused(Step):
+                def run(self, stream=None):
+                    for mt in use:
+                        if silu:
+                            gemm.run_split(stream, m, mt, xg, yf, Epi.Plain, True, ldx=17408)
+                            lora_silu(stream, xa, 1, cols, b, rank, rows, tab, slot, scale, m, yf, mid)
+                        else:
+                            gemm.run(stream, m, mt, xg, yf, Epi.Plain, ldx=17408)
+                            lora_add(stream, xa, 1, cols, b, rank, rows, tab, slot, scale, m, yf)
+
+            class Bare(Step):
+                def run(self, stream=None):
+                    for mt in use:
+                        gemm.run(stream, m, mt, xg, mid if silu else yf, Epi.Silu if silu else Epi.Plain, ldx=17408)
+
+            r = {}
+            for tag, cls in (("fused", Fused), ("unfused", Unfused), ("no_adapter", Bare)):
+                st = cls(gemm, m, 8)
+                ms = time_step(st, args.steps if m == 1 else 20, 3, not args.no_graph, per_graph=2 if m == 1 else 1,
+                               min_reps=100 if m == 1 else 20)
+                r[tag + "_us"] = round(ms * 1e3 / len(use), 2)
+            res[name] = r
+        out[f"m{m}"] = res
+        print(f"# LoRA rank {rank} M={m}: {res} (us per product)", file=sys.stderr, flush=True)
+    return {"lora_27b": out}
+
+
 def config0_line(gemm, args):
     """BASELINE.json configs[0] on the GPU: the single int4 GEMV M=1, K=2560, N=9728, symmetric, over 48 distinct
     device copies (617 MB per pass, beyond the 256 MB MALL) in HIP graphs: HBM GB/s over the algorithmic bytes."""
@@ -558,7 +622,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of lines: m1,m5,prefill,pfzp,pfshort,int8,i8g,dense,dequant,set4b,c0,consumers")
+                    help="comma list of lines: m1,m5,prefill,pfzp,pfshort,int8,i8g,dense,dequant,set4b,c0,consumers,"
+                         "lora")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -602,7 +667,7 @@ def main():
         print(json.dumps({"set4b_run": "done"}))
         return
     only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "pfzp", "pfshort", "int8", "i8g", "dense",
-                                                         "dequant", "set4b", "c0", "consumers"}
+                                                         "dequant", "set4b", "c0", "consumers", "lora"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
@@ -709,6 +774,8 @@ def main():
         extra.update(consumers_line(args))
     if "c0" in only:
         extra.update(config0_line(gemm, args))
+    if "lora" in only:
+        extra.update(lora_line(gemm, args))
     if "i8g" in only:
         extra.update(grouped_int8_line(gemm, args))
     if "pfzp" in only:

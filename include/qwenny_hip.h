@@ -192,6 +192,31 @@ size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, s
 int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, const int32_t* out_rows,
             size_t n_out, void* y, int epi, uint64_t* keys, int whole);
 
+/* An unmerged LoRA adapter on a product (the arguments of the reference's lora_add / lora_silu kernels,
+ * kernels/lora.cuh:52-113, src/cuda/qwen/lora.rs:143-190): xa, the stacked A product's partials f32
+ * [split][n][m_cols] (m_cols <= 256) of the product's n tokens; b_f16, B f16 [rows][rank] in the product's row order
+ * (rank 8, 16, 32 or 64); tab, 8 int32: each module's end row (ascending; unused INT_MAX), then its first column of xa
+ * (-1: not adapted); for a SwiGLU product module 0 is the gate and 1 the up rows; the token's slot scale
+ * slot_scale[tok_slot[t]] (0: no delta). All device pointers. */
+typedef struct qh_lora {
+    const float* xa;
+    int32_t split;
+    int32_t m_cols;
+    const uint16_t* b_f16;
+    int32_t rank;
+    const int32_t* tab;
+    const int32_t* tok_slot;
+    const float* slot_scale;
+} qh_lora;
+
+/* qh_gemm with the LoRA delta s_t * B (A x) fused into the product's epilogue, computed in f32: QH_EPI_PLAIN adds it to
+ * split 0 of the partials (what qh_gemm then qh_lora_add on y[0] make); QH_EPI_SILU adds it to gate and up before the
+ * activation (what a whole plain product, then qh_lora_silu, make), with no f32 [gate; up] pass through memory.
+ * Outputs whose delta is exactly zero (unadapted rows, tokens of slot scale 0) are the product's bit for bit.
+ * QH_EPI_ARGMAX takes no adapter (QH_EINVAL). lora NULL: qh_gemm. Returns the split or < 0. Launch only. */
+int qh_gemm_lora(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, void* y, int epi,
+                 int whole, const qh_lora* lora);
+
 /* qh_gemm without allocation: no counterpart in the reference. For callers that cannot allocate device memory around
  * a product (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments,
  * checks, launch plans and results as qh_gemm, but the launch scratch (argmax table, stream-K partials and counters)

@@ -24,6 +24,13 @@ class MatDesc(ctypes.Structure):
                 ("scale_bytes", S), ("zero_bytes", S), ("per_channel", ctypes.c_int32)]
 
 
+class LoraC(ctypes.Structure):
+    """qh_lora (the reference's lora_add / lora_silu arguments)"""
+
+    _fields_ = [("xa", P), ("split", ctypes.c_int32), ("m_cols", ctypes.c_int32), ("b_f16", P),
+                ("rank", ctypes.c_int32), ("tab", P), ("tok_slot", P), ("slot_scale", P)]
+
+
 # name -> (restype, argtypes); every symbol include/qwenny_hip.h declares
 SIGNATURES = {
     "qh_last_error": (ctypes.c_char_p, []),
@@ -57,6 +64,7 @@ SIGNATURES = {
     "qh_part_len": (S, [P, P, S, S]),
     "qh_gemm": (I, [P, P, P, P, S, S, P, S, P, I, P, I]),
     "qh_gemm_noalloc": (I, [P, P, P, P, S, S, P, S, P, I, P, I]),
+    "qh_gemm_lora": (I, [P, P, P, P, S, S, P, I, I, ctypes.POINTER(LoraC)]),
     "qh_put_block": (I, [P, P, P, ctypes.POINTER(QuantC), P, S, P]),
 }
 

@@ -176,6 +176,17 @@ class Gemm:
         return check(lib().qh_gemm(self._ctx, _stream(stream), w._m, _ptr(x), ldx, n, _ptr(out_rows), n_out, _ptr(y),
                                    int(epi), _ptr(keys), int(whole)))
 
+    def run_lora(self, stream, n, w, x, y, epi, lora, whole=False, ldx=0):
+        """run / run_split with an unmerged LoRA adapter's delta fused into the epilogue: `lora` = (xa, split, m_cols,
+        b_f16, rank, tab, tok_slot, slot_scale) as lora_add takes them (device tensors). Plain: the delta on split 0;
+        Silu: added to gate and up before the activation. Returns the split."""
+        from ._lib import LoraC
+
+        xa, split, m_cols, b, rank, tab, tok_slot, slot_scale = lora
+        lc = LoraC(_ptr(xa), split, m_cols, _ptr(b), rank, _ptr(tab), _ptr(tok_slot), _ptr(slot_scale))
+        return check(lib().qh_gemm_lora(self._ctx, _stream(stream), w._m, _ptr(x), ldx, n, _ptr(y), int(epi),
+                                        int(whole), ctypes.byref(lc)))
+
     def put_block(self, stream, m, q, zeros, block, rows):
         """Write stored rows `rows` (16) of `q` as the 16-row block `block` of a matrix from Mat.marlin_rows, counting
         it as valid (src/cuda/core.rs:619-657)."""

@@ -383,7 +383,7 @@ extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size
 // qh_gemm's checks and launch, with the scratch (argmax table and counter, stream-K partials and counters) at `sc`.
 int qh::gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
                           const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole,
-                          const Scratch& sc) {
+                          const Scratch& sc, const qh_lora* lora) {
     if (!ctx || !w || !x || !y) return fail(QH_EINVAL, "gemm: null");
     if (epi != QH_EPI_PLAIN && epi != QH_EPI_SILU && epi != QH_EPI_ARGMAX) return fail(QH_EINVAL, "epilogue %d", epi);
     if (epi == QH_EPI_ARGMAX && !keys) return fail(QH_EINVAL, "argmax without keys");
@@ -401,6 +401,23 @@ int qh::gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void
     if (m > (size_t)SKINNY_MAX_M && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
         return fail(QH_EINVAL, "gemm: %zu token rows of %zu elements: x must fit in 4 GiB", n, ldx);
     Launch l = make_launch(ctx, w, x, ldx, m, out_rows, y, epi, keys, whole, stream, sc);
+    if (lora) {
+        if (epi == QH_EPI_ARGMAX) return fail(QH_EINVAL, "gemm lora: the argmax epilogue takes no adapter");
+        if (!lora->xa || !lora->b_f16 || !lora->tab || !lora->tok_slot || !lora->slot_scale || lora->split < 1)
+            return fail(QH_EINVAL, "gemm lora: null or %d splits", lora->split);
+        if (lora->rank != 8 && lora->rank != 16 && lora->rank != 32 && lora->rank != 64)
+            return fail(QH_EINVAL, "LoRA rank %d: ranks 8, 16, 32 and 64 are served", lora->rank);
+        if (lora->m_cols < 1 || lora->m_cols > 256)
+            return fail(QH_EINVAL, "gemm lora: %d columns of xa (at most 256)", lora->m_cols);
+        l.lora_xa = lora->xa;
+        l.lora_split = lora->split;
+        l.lora_cols = lora->m_cols;
+        l.lora_rank = lora->rank;
+        l.lora_b = lora->b_f16;
+        l.lora_tab = lora->tab;
+        l.lora_tok_slot = lora->tok_slot;
+        l.lora_slot_scale = lora->slot_scale;
+    }
     hipError_t e = launch(l);
     if (e != hipSuccess) return fail(QH_EHIP, "gemm launch: %s", hipGetErrorString(e));
     return l.split;
@@ -411,6 +428,13 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
     if (!ctx) return fail(QH_EINVAL, "gemm: null");
     return gemm_with_scratch(ctx, stream, w, x, ldx, n, out_rows, n_out, y, epi, keys, whole,
                              Scratch{ctx->argmax_scratch, ctx->sk_scratch});
+}
+
+extern "C" int qh_gemm_lora(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, void* y,
+                            int epi, int whole, const qh_lora* lora) {
+    if (!ctx) return fail(QH_EINVAL, "gemm lora: null");
+    return gemm_with_scratch(ctx, stream, w, x, ldx, n, nullptr, 0, y, epi, nullptr, whole,
+                             Scratch{ctx->argmax_scratch, ctx->sk_scratch}, lora);
 }
 
 extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros,

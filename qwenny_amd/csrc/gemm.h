@@ -11,7 +11,7 @@ namespace qh {
 // qh_gemm's argument checks and launch, with the launch scratch at `sc` (device addresses; zero between launches).
 int gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
                       const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole,
-                      const Scratch& sc);
+                      const Scratch& sc, const qh_lora* lora = nullptr);
 
 // The device a context was opened on.
 int ctx_device(const qh_ctx* ctx);

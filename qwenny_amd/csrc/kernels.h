@@ -49,6 +49,14 @@ struct Launch {
     // plain prefill products of few tokens: whole items cut into ks slices of K, slice s writing partial y[s] (the
     // split-K contract; ks = 1: none). whole: the caller wants one partial. dry_run: plan only (l.split), no launch.
     int ks, whole, dry_run;
+    // an unmerged LoRA adapter's delta fused into the epilogue (lora_rank 0: none): plain products add it to split 0,
+    // SwiGLU products to gate and up before the activation (kernels.hip lora_delta16 / lora_delta32)
+    const float* lora_xa;        // the stacked A product's partials [lora_split][m][lora_cols]
+    int lora_split, lora_cols, lora_rank;
+    const uint16_t* lora_b;      // B f16 [rows][lora_rank], the product's row order
+    const int* lora_tab;         // module end rows (3 used), then each module's first column of xa (-1: none)
+    const int* lora_tok_slot;
+    const float* lora_slot_scale;
     uint32_t bf16_magic;    // 0x43004300: the bf16 pair (128, 128) (see kernels.hip i4_biased)
     uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;

@@ -32,6 +32,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Kernel format F: bit flags of the storage (kernels.h F_*).
 
@@ -181,6 +182,125 @@ __device__ __forceinline__ int zero_of(const uint16_t* zeros, int tile, int G, i
 // (every wave of it reads them with ds_read_b128 instead of fetching them from L2). The grid's y dimension splits the
 // super-chunks of K (plain products: split-K partials); WK waves' partial sums are reduced through LDS.
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// The LoRA delta fused into the products' epilogues (the reference applies it as separate kernels after the product,
+// kernels/lora.cuh:52-113): delta[t][o] = s_t B[o] . xa_t[off(o) .. off(o) + R), s_t the token's slot scale, xa_t the
+// token's A product summed over its split-K partials, off(o) the first column of o's module (routing as
+// lora_module: module ends tab[0..2], column offsets tab[4..7]; SwiGLU products: rows 0..7 of each 16-row tile are
+// the gate (tab[4]), rows 8..15 the up rows (tab[5])). It runs on the f32 matrix cores, in the layout of each kernel's
+// accumulators: D = (s xa) (tokens x R) . B^T (R x outputs), the contraction index laid out so that a lane group
+// reads contiguous runs of xa and B. A tile (or 32-row block) that straddles a module end takes one pass per module
+// with the other rows' B masked to zero. The MFMAs accumulate straight into the product's accumulators (no registers
+// held for a separate delta): rows of unadapted modules are not touched, and the products of tokens of slot scale 0
+// or of masked rows add exact zeros.
+
+template <bool SILU>
+__device__ __forceinline__ int lora_module_of(const Launch& a, int o) {
+    if (SILU) return (o >> 3) & 1;  // gate / up halves of a 16-row tile
+    return (o >= a.lora_tab[0]) + (o >= a.lora_tab[1]) + (o >= a.lora_tab[2]);
+}
+__device__ __forceinline__ int lora_off(const Launch& a, int m) { return a.lora_tab[4 + m]; }
+
+// s_t * sum over splits of xa[.][tok][c .. c + N), N consecutive columns into v
+template <int N>
+__device__ __forceinline__ void lora_xs_run(const Launch& a, int tok, int c, float s, float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = 0.0f;
+    for (int sp = 0; sp < a.lora_split; sp++) {
+        const float* p = a.lora_xa + ((size_t)sp * a.m + tok) * a.lora_cols + c;
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += p[i];
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] *= s;
+}
+
+// B[o][c .. c + N) (f16 -> f32), zero when `keep` is false
+template <int N>
+__device__ __forceinline__ void lora_b_run(const Launch& a, int o, int c, bool keep, float (&v)[N]) {
+    const _Float16* p = (const _Float16*)a.lora_b + (size_t)o * a.lora_rank + c;
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = keep ? (float)p[i] : 0.0f;
+}
+
+__device__ __forceinline__ float lora_scale_of(const Launch& a, int tok) {
+    return a.lora_slot_scale[a.lora_tok_slot[tok]];
+}
+
+// The decode kernel's layout (v_mfma_f32_16x16x4_f32): the delta of 16-row tile `tile` for 16 tokens starting at
+// tok0 (A rows: tokens tok0 + lane % 16, clamped to m - 1); lane l gets D[token tok0 + 4 (l / 16) + i][row l % 16].
+template <bool SILU>
+__device__ void lora_delta16(const Launch& a, int tile, int tok0, f32x4& d) {
+    constexpr int C = 2;  // steps whose operands are in registers at a time (R / 4 is a multiple)
+    const int Q = a.lora_rank / 4;  // contraction steps; lane group q takes k = q Q + i
+    const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
+    const int o = tile * TILE + l16, mod = lora_module_of<SILU>(a, o);
+    const int mlo = lora_module_of<SILU>(a, tile * TILE), mhi = lora_module_of<SILU>(a, tile * TILE + TILE - 1);
+    const int tok = min(tok0 + l16, a.m - 1);
+    const float s = lora_scale_of(a, tok);
+    for (int m = mlo; m <= mhi; m++) {
+        const int c0 = lora_off(a, m);
+        if (c0 < 0) continue;  // wave-uniform
+        for (int i0 = 0; i0 < Q; i0 += C) {
+            float xv[C], bv[C];
+            lora_xs_run<C>(a, tok, c0 + q * Q + i0, s, xv);
+            lora_b_run<C>(a, o, q * Q + i0, mod == m, bv);
+#pragma unroll
+            for (int i = 0; i < C; i++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], bv[i], d, 0, 0, 0);
+        }
+    }
+}
+
+// The prefill kernel's layout (v_mfma_f32_32x32x2_f32): the deltas of a wave's TN blocks of 32 output rows (block t:
+// rows (tile0 + 2 t) 16 ..) for its BMB blocks of 32 tokens (block bb: tokens tok0 + 32 bb ..), accumulated into
+// acc[bb][t]; lane l holds D[token 8 (v / 4) + 4 (l / 32) + v % 4][row l % 32], v = 0..15. Loads are batched for
+// latency: the tokens' slot scales for every block at once, each output block's B run once, the xa runs of NBB token
+// blocks at a time.
+template <bool SILU, int BMB, int TN>
+__device__ void lora_item32(const Launch& a, int tile0, int tok0, f32x16 (&acc)[BMB][TN]) {
+    // one code path for every rank (a switch over ranks multiplies the epilogue's code and spills registers): the
+    // H = R / 2 contraction steps run C at a time, lane group h taking k = h H + i
+    constexpr int C = 4;                     // steps whose operands are in registers at a time (H is a multiple)
+    constexpr int NBB = BMB < 4 ? BMB : 4;   // token blocks whose xa runs are loaded together
+    const int H = a.lora_rank / 2;
+    const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+    int tok[BMB];
+    float s[BMB];
+#pragma unroll
+    for (int bb = 0; bb < BMB; bb++) tok[bb] = min(tok0 + 32 * bb + l32, a.m - 1);
+#pragma unroll
+    for (int bb = 0; bb < BMB; bb++) s[bb] = (float)a.lora_tok_slot[tok[bb]];  // slot index, exact as a float
+#pragma unroll
+    for (int bb = 0; bb < BMB; bb++) s[bb] = a.lora_slot_scale[(int)s[bb]];
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        const int o0 = (tile0 + 2 * t) * TILE;
+        if (o0 >= a.rows) break;  // wave-uniform
+        const int o = min(o0 + l32, a.rows - 1), mod = lora_module_of<SILU>(a, o);
+        const int mlo = lora_module_of<SILU>(a, o0), mhi = lora_module_of<SILU>(a, min(o0 + 31, a.rows - 1));
+        for (int m = mlo; m <= mhi; m++) {
+            const int c0 = lora_off(a, m);
+            if (c0 < 0) continue;  // wave-uniform
+            for (int i0 = 0; i0 < H; i0 += C) {
+                float bv[C];
+                lora_b_run<C>(a, o, h * H + i0, mod == m && o0 + l32 < a.rows, bv);
+                // (loops over accumulators fully unrolled: an indexed register array would live in scratch memory)
+#pragma unroll
+                for (int b0 = 0; b0 < BMB; b0 += NBB) {
+                    float xv[NBB][C];
+#pragma unroll
+                    for (int j = 0; j < NBB; j++) lora_xs_run<C>(a, tok[b0 + j], c0 + h * H + i0, s[b0 + j], xv[j]);
+#pragma unroll
+                    for (int j = 0; j < NBB; j++)
+#pragma unroll
+                        for (int i = 0; i < C; i++)
+                            acc[b0 + j][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[j][i], bv[i], acc[b0 + j][t], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
 
 template <int F, int EPI, int NR, int T, int NG, int TB>
 __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) {
@@ -372,6 +492,23 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
     }
 
     const int sp = blockIdx.y;
+    // the LoRA delta: on split 0 of a plain product, before the activation of a SwiGLU one
+    if ((EPI == EPI_SILU || (EPI == EPI_PLAIN && sp == 0)) && a.lora_rank && lead) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const int tile = tile0 + t;
+            if (tile >= tiles) break;
+#pragma unroll
+            for (int b = 0; b < TB; b++) {
+                f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int r = 0; r < NR; r++) d[r] = acc[b][t][r];
+                lora_delta16<EPI == EPI_SILU>(a, tile, 16 * b, d);
+#pragma unroll
+                for (int r = 0; r < NR; r++) acc[b][t][r] = d[r];
+            }
+        }
+    }
     unsigned long long key[TB][NR];
 #pragma unroll
     for (int b = 0; b < TB; b++)
@@ -443,8 +580,6 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
 // device-scope atomic); the one that counts last adds the partials in segment order (so the sum does not depend on
 // who arrives last), runs the epilogue and clears the counter. No workgroup ever waits for another.
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
 }
@@ -471,7 +606,7 @@ __device__ __forceinline__ int sk_owner(int u, int q, int r) {
     return u < r * (q + 1) ? u / (q + 1) : r + (u - r * (q + 1)) / q;
 }
 
-template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB>
+template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB, bool LORA>
 __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     constexpr int BM = WM * BMB * 32;                // tokens per workgroup
     constexpr int WTILES = WN * TN * 2;              // 16-row tiles per workgroup
@@ -650,9 +785,22 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // epilogue of the current item: acc[bb][t][v] = D[token tok0 + wtok0 + 32 bb + 8 (v / 4) + 4 lh + v % 4]
     // [output 32-block t, l32]
     auto epilogue = [&]() {
-        float rs[TN];
+        if (F & F_PERCH) {  // the row's scale after the exact integer sum
 #pragma unroll
-        for (int t = 0; t < TN; t++) rs[t] = (F & F_PERCH) ? scale_of<F>(a.scales, tt[t], G, 0, l16) : 1.0f;
+            for (int t = 0; t < TN; t++) {
+                const float rs = scale_of<F>(a.scales, tt[t], G, 0, l16);
+#pragma unroll
+                for (int bb = 0; bb < BMB; bb++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[bb][t][e] *= rs;
+            }
+        }
+        // the LoRA delta: on partial 0 of a plain product, before the activation of a SwiGLU one
+        if constexpr (LORA) {
+            if (EPI == EPI_SILU || kslice == 0) {
+                lora_item32<EPI == EPI_SILU, BMB, TN>(a, tile0, tok0 + wtok0, acc);
+            }
+        }
         unsigned long long key[BMB][16];
 #pragma unroll
         for (int bb = 0; bb < BMB; bb++)
@@ -668,7 +816,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                     const int tok = tok0 + wtok0 + 32 * bb + 8 * (v >> 2) + 4 * lh + (v & 3);
-                    const float val = (F & F_PERCH) ? acc[bb][t][v] * rs[t] : acc[bb][t][v];
+                    const float val = acc[bb][t][v];
                     if (EPI == EPI_SILU) {
                         const float up = __shfl_xor(val, 8);
                         if (tile_ok && l16 < 8 && tok < M)
@@ -834,8 +982,8 @@ static long prefill_plan(Launch& l) {
     // resident workgroups per CU (per instantiation; the same on every MI355X; thread-safe static initialisation)
     static const int per_cu = [] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>, threads,
-                                                         0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB, false>,
+                                                         threads, 0) != hipSuccess)
             n = 0;
         return n;
     }();
@@ -887,7 +1035,14 @@ template <int F, int EPI, int BMB, int TN, int WM, int WN, int MINB = 1>
 static hipError_t prefill_cfg(Launch& l) {
     (void)prefill_plan<F, EPI, BMB, TN, WM, WN, MINB>(l);
     if (l.dry_run) return hipSuccess;
-    hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB>), dim3(l.dp_items + l.sk_wgs),
+    // the LoRA epilogue in kernels of its own (its code would otherwise weigh on every product's registers)
+    if constexpr (EPI == EPI_PLAIN || EPI == EPI_SILU)
+        if (l.lora_rank) {
+            hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB, true>), dim3(l.dp_items + l.sk_wgs),
+                               dim3(WM * WN * 64), 0, l.stream, l);
+            return hipGetLastError();
+        }
+    hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB, false>), dim3(l.dp_items + l.sk_wgs),
                        dim3(WM * WN * 64), 0, l.stream, l);
     return hipGetLastError();
 }
