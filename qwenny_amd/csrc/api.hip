@@ -29,6 +29,7 @@ struct qh_ctx {
     // QH_PF_SK=0 turns it off, a value above 1 replaces the launcher's fix-up cost (tuning)
     void* sk_scratch;
     int stream_k;
+    int skinny_plain_wk;    // skinny kernel, plain products: wave rows over K per workgroup (1; QH_SKINNY_PLAIN_WK)
 };
 
 int qh::ctx_device(const qh_ctx* ctx) { return ctx->device; }
@@ -93,7 +94,8 @@ extern "C" int qh_open(int device, qh_ctx** out) {
     *out = new qh_ctx{device, scratch, std::max(cus, 1), std::min(16, std::max(1, env_int("QH_SKINNY_MAX_W", 16))),
                       std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
-                      std::min(9, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1))};
+                      std::min(9, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1)),
+                      std::min(4, std::max(1, env_int("QH_SKINNY_PLAIN_WK", 1)))};
     return QH_OK;
 }
 
@@ -287,6 +289,9 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
     const int want_wt = ctx->skinny_tile_waves > 0 ? ctx->skinny_tile_waves : (tokens <= 2 ? 4 : 8);
     if (plain) {
         const int wt = std::max(1, std::min({want_wt, cols, tokens > 16 ? 8 : 16}));
+        // QH_SKINNY_PLAIN_WK (tuning): wave rows over K within the workgroup, dividing the partials
+        const int pk = ctx->skinny_plain_wk;
+        if (pk > 1 && (G / ng) % pk == 0 && wt * pk <= 16) return Partition{wt, wt * pk, G / ng / pk, ng};
         return Partition{wt, wt, G / ng, ng};
     }
     const size_t per_group = std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's activations
@@ -347,6 +352,9 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
         l.waves = p.waves;
         l.split = p.split;
         l.groups_per_wave = p.groups_per_wave;
+        // 16-byte row runs need a 16-byte aligned y (its rows are: the row count is a multiple of 16)
+        // (one token: the LDS round trip costs more than it saves, measured 3% on small matrices)
+        l.stage_out = epi == QH_EPI_PLAIN && m > 1 && ((uintptr_t)y & 15) == 0 && p.waves == p.tile_waves;
     } else {
         l.tile_waves = 4;
         l.waves = 4;

@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "kernels.h"
 #include "layout.h"
 
@@ -514,7 +516,29 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
     for (int b = 0; b < TB; b++)
 #pragma unroll
         for (int r = 0; r < NR; r++) key[b][r] = 0;
-    if (lead) {
+    if (EPI == EPI_PLAIN && a.stage_out) {
+        // plain partials through LDS: the wave's block (m tokens x T 16-row tiles) is written to its own LDS slot in
+        // the MFMA layout and read back along the rows, so that y is written with 16-byte stores of whole row runs
+        // (one store instruction for up to 8 tokens, against one per tile and token row of 16 lanes: small scattered
+        // stores cost far more per byte than the reads they follow)
+        constexpr int RW = T * TILE;  // rows of the wave's block
+        float* stg = red + (size_t)wave * M * RW;
+#pragma unroll
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int b = 0; b < TB; b++)
+#pragma unroll
+                for (int r = 0; r < NR; r++) {
+                    const int tok = 16 * b + 4 * kq + r;
+                    if (tok < M) stg[tok * RW + t * TILE + l16] = acc[b][t][r];
+                }
+        const int row0 = tile0 * TILE;
+        for (int i = lane; i < M * (RW / 4); i += 64) {
+            const int tok = i / (RW / 4), c = 4 * (i - tok * (RW / 4));
+            if (row0 + c < a.rows)
+                *(f32x4*)((float*)a.y + ((size_t)sp * M + tok) * a.ldy + row0 + c) = *(const f32x4*)(stg + tok * RW + c);
+        }
+    } else if (lead) {
 #pragma unroll
         for (int t = 0; t < T; t++) {
             const int tile = tile0 + t;
@@ -1103,7 +1127,10 @@ template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(Launch& l);
 size_t skinny_lds(const Launch& l) {
     const int wk = l.waves / l.tile_waves, tb = (l.m + 15) / 16;
     const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
-    return x + (size_t)(wk - 1) * l.tile_waves * tb * SKINNY_TILES * 4 * 64 * sizeof(float);
+    const size_t red = (size_t)(wk - 1) * l.tile_waves * tb * SKINNY_TILES * 4 * 64 * sizeof(float);
+    // plain partials staged per wave: m tokens x SKINNY_TILES tiles of f32
+    const size_t out = l.stage_out ? (size_t)l.waves * l.m * SKINNY_TILES * TILE * sizeof(float) : 0;
+    return x + std::max(red, out);
 }
 
 template <int F>
