@@ -384,9 +384,9 @@ def consumers_line(args):
             "add_rmsnorm": (lambda: add_rmsnorm(None, h, x, split, m, hid, w, yb),
                             (split + 2) * m * hid * 4 + hid * 4 + m * hid * 2),
             "lora_add": (lambda: lora_add(None, xa, 1, mcols, b, rank, hid, tab_add, slot, scale, m, ys),
-                         m * mcols * 4 + hid * rank * 2 * -(-m // 8) + 2 * m * hid * 4),
+                         m * mcols * 4 + hid * rank * 2 * -(-m // 16) + 2 * m * hid * 4),
             "lora_silu": (lambda: lora_silu(None, xa, 1, mcols, b, rank, gu, tab_silu, slot, scale, m, ygu, mid),
-                          m * mcols * 4 + gu * rank * 2 * -(-m // 8) + m * gu * 4 + m * gu),
+                          m * mcols * 4 + gu * rank * 2 * -(-m // 16) + m * gu * 4 + m * gu),
         }
         for name, (fn, nbytes) in cases.items():
             for _ in range(3):

@@ -255,7 +255,8 @@ int qh_add_rmsnorm(void* stream, float* h, const float* x, int splits, size_t n,
  * added). xa: the stacked A product's partials f32 [split][n][m_cols] (m_cols <= 256); b_f16: B f16 [rows][rank] in
  * the product's row order (rank 8, 16, 32 or 64; 16-byte aligned); tab: 8 int32, each module's end row (ascending;
  * unused INT_MAX), then its first column of xa (-1: not adapted; a column range must lie within m_cols). rows: a
- * multiple of 16 (the products' row count). All pointers are device addresses. The delta is computed in f32.
+ * multiple of 16 (the products' row count). y 16-byte aligned with ldy a multiple of 4, mid 8-byte aligned (QH_EINVAL
+ * otherwise). All pointers are device addresses. The delta is computed in f32.
  * lora_add: y [n][ldy] f32, the plain product's split 0, row o += s_t * B[o] . xa[t][off(o) ..].
  * lora_silu: y [n][ldy] f32, a plain [gate; up] product packed in row_order(rows, 1) (split 1), read; mid [n][rows / 2]
  * bf16 = silu(gate + delta) * (up + delta) for every token t < n, as the SwiGLU epilogue writes it.

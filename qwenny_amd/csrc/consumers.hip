@@ -134,8 +134,8 @@ __global__ __launch_bounds__(T) void add_rmsnorm_kernel(float* __restrict__ h, c
 // accumulators have: lane l holds D[token 4 (l / 16) + i][row l % 16], i = 0..3.
 //
 // A workgroup takes WT * 64 rows (LORA_WAVES waves of WT tiles each: 4 for 17 tokens and more, 1 for fewer, where the
-// launch would otherwise have too few waves) and up to LORA_TOK tokens (one 16-token block: at most 33 KiB of LDS, so
-// that several workgroups per CU hide each other's memory round trips). The deltas go through LDS so that y is read and written along its rows (whole
+// launch would otherwise have too few waves) and up to LORA_TOK tokens (one 16-token block). The deltas reuse the LDS
+// of the staged xa (at most 17 KiB per workgroup), so that 8 workgroups per CU hide each other's memory round trips. The deltas go through LDS so that y is read and written along its rows (whole
 // cache lines), not in the MFMA's 16-row pieces.
 
 constexpr int LORA_COLS_MAX = 256;  // columns of xa at most (four modules of rank 64)
@@ -239,14 +239,17 @@ struct LoraTiles {
         }
     }
 
+    // xs and dl are the same LDS: every wave's MFMAs read xs before any delta is written
     template <class ModuleOf>
-    __device__ void deltas(const LoraArgs& a, int o0, int tn, const float* xs, const int* off, ModuleOf module_of,
+    __device__ void deltas(const LoraArgs& a, int o0, const float* xs, const int* off, ModuleOf module_of,
                            float* dl) const {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, q = lane >> 4;
+        lf32x4 d[WT];
 #pragma unroll
         for (int wt = 0; wt < WT; wt++) {
             const int r0 = (wave * WT + wt) * 16;  // tile's first row in the workgroup
-            if (o0 + r0 >= a.rows) break;               // wave-uniform
+            d[wt] = lf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (o0 + r0 >= a.rows) continue;            // wave-uniform
             const int mod = module_of(o0 + r0 + l16), mlo = module_of(o0 + r0), mhi = module_of(o0 + r0 + 15);
             float bv[R / 4];
 #pragma unroll
@@ -254,7 +257,6 @@ struct LoraTiles {
                 bv[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[wt][i] & 0xffffu));
                 bv[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[wt][i] >> 16));
             }
-            lf32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int m = mlo; m <= mhi; m++) {
                 const int c0 = off[m];
                 if (c0 < 0) continue;  // wave-uniform: module not adapted
@@ -262,83 +264,110 @@ struct LoraTiles {
                 const float* xr = xs + l16 * LORA_XS_LD + c0 + q * (R / 4);
 #pragma unroll
                 for (int i = 0; i < R / 4; i++)
-                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(xr[i], mine ? bv[i] : 0.0f, d, 0, 0, 0);
+                    d[wt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xr[i], mine ? bv[i] : 0.0f, d[wt], 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < 4; i++) dl[(4 * q + i) * DL_LD + r0 + l16] = d[i];
         }
-        (void)tn;
+        __syncthreads();
+#pragma unroll
+        for (int wt = 0; wt < WT; wt++) {
+            const int r0 = (wave * WT + wt) * 16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) dl[(4 * q + i) * DL_LD + r0 + l16] = d[wt][i];
+        }
         __syncthreads();
     }
 };
 
 // y [n][ldy] (a plain product's split 0) row o += delta for the adapter tokens; rows of unadapted modules and tokens
-// without the adapter are left as they are. Thread i owns row o0 + i % ROWS of tokens i / ROWS + (256 / ROWS) k.
+// without the adapter are left as they are. Thread i owns rows o0 + 4 (i % QUADS) .. + 3 (one 16-byte access per
+// token) of tokens i / QUADS + TS k.
 template <int R, int WT>
 __global__ __launch_bounds__(64 * LORA_WAVES) void lora_add_kernel(LoraArgs a, float* __restrict__ y) {
-    constexpr int ROWS = WT * 64, DL_LD = lora_dl_ld<WT>(), TS = 64 * LORA_WAVES / ROWS, TPT = LORA_TOK / TS;
-    __shared__ float xs[LORA_TOK * LORA_XS_LD];
-    __shared__ float dl[LORA_TOK * DL_LD];
+    constexpr int ROWS = WT * 64, QUADS = ROWS / 4, DL_LD = lora_dl_ld<WT>(), TS = 64 * LORA_WAVES / QUADS,
+                  TPT = LORA_TOK / TS;
+    __shared__ float xs[LORA_TOK * (LORA_XS_LD > DL_LD ? LORA_XS_LD : DL_LD)];  // the staged xa, then the deltas
+    float* const dl = xs;
     __shared__ float sc[LORA_TOK];
     const int t0 = blockIdx.y * LORA_TOK, o0 = blockIdx.x * ROWS;
     const int tn = min(LORA_TOK, a.n - t0);
-    const int c = threadIdx.x % ROWS, tp = threadIdx.x / ROWS, o = min(o0 + c, a.rows - 1);
+    const int c = 4 * (threadIdx.x % QUADS), tp = threadIdx.x / QUADS, o = min(o0 + c, a.rows - 4);
     LoraTiles<R, WT> tiles;
     tiles.load(a, o0);
-    float v[TPT];
+    float4 v[TPT];
     float* yc = y + (size_t)t0 * a.ldy + o;
 #pragma unroll
     for (int k = 0; k < TPT; k++) {
-        const int t = tp + TS * k;
-        v[k] = t < tn ? yc[(size_t)t * a.ldy] : 0.0f;
+        const int t = min(tp + TS * k, tn - 1);
+        v[k] = *(const float4*)(yc + (size_t)t * a.ldy);
     }
     lora_stage_xs(a, t0, xs, sc);
     const int off[4] = {a.tab[4], a.tab[5], a.tab[6], a.tab[7]};
-    tiles.deltas(a, o0, tn, xs, off, [&](int r) { return lora_module(a.tab, r); }, dl);
-    if (o0 + c >= a.rows || off[lora_module(a.tab, o)] < 0) return;
+    tiles.deltas(a, o0, xs, off, [&](int r) { return lora_module(a.tab, r); }, dl);
+    if (o0 + c >= a.rows) return;
+    bool ad[4];  // rows of adapted modules (the others keep their bits, -0.0 included)
+#pragma unroll
+    for (int i = 0; i < 4; i++) ad[i] = off[lora_module(a.tab, o + i)] >= 0;
+    if (!(ad[0] | ad[1] | ad[2] | ad[3])) return;
 #pragma unroll
     for (int k = 0; k < TPT; k++) {
         const int t = tp + TS * k;
-        if (t < tn && sc[t] != 0.0f) yc[(size_t)t * a.ldy] = v[k] + dl[t * DL_LD + c];
+        if (t >= tn || sc[t] == 0.0f) continue;
+        const float4 d = *(const float4*)(dl + t * DL_LD + c);
+        float4 r = v[k];
+        r.x = ad[0] ? r.x + d.x : r.x;
+        r.y = ad[1] ? r.y + d.y : r.y;
+        r.z = ad[2] ? r.z + d.z : r.z;
+        r.w = ad[3] ? r.w + d.w : r.w;
+        *(float4*)(yc + (size_t)t * a.ldy) = r;
     }
 }
 
 // mid [n][rows / 2] (bf16) = SwiGLU of the plain [gate; up] product y [n][ldy] (split 1, packed in the SwiGLU
 // epilogue's row order: 16-row tile p holds gate rows 8p .. 8p + 7, then their up rows) with the delta added first:
 // in a tile, rows 0..7 are module 0 (gate, columns from tab[4]) and rows 8..15 module 1 (up, tab[5]). Thread i owns
-// output j = i % (ROWS / 2) of the workgroup's (gate row 16 (j / 8) + j % 8, up row + 8) for tokens
-// i / (ROWS / 2) + TS k.
+// outputs j .. j + 3, j = 4 (i % OQ), of the workgroup (gate rows 16 (j / 8) + j % 8 .. + 3, up rows 8 further: one
+// 16-byte load each, one 8-byte store) for tokens i / OQ + TS k.
 template <int R, int WT>
 __global__ __launch_bounds__(64 * LORA_WAVES) void lora_silu_kernel(LoraArgs a, const float* __restrict__ y,
                                                                    __bf16* __restrict__ mid) {
-    constexpr int ROWS = WT * 64, DL_LD = lora_dl_ld<WT>(), TS = 64 * LORA_WAVES / (ROWS / 2), TPT = LORA_TOK / TS;
-    __shared__ float xs[LORA_TOK * LORA_XS_LD];
-    __shared__ float dl[LORA_TOK * DL_LD];
+    constexpr int ROWS = WT * 64, OQ = ROWS / 8, DL_LD = lora_dl_ld<WT>(), TS = 64 * LORA_WAVES / OQ,
+                  TPT = TS < LORA_TOK ? LORA_TOK / TS : 1;
+    __shared__ float xs[LORA_TOK * (LORA_XS_LD > DL_LD ? LORA_XS_LD : DL_LD)];  // the staged xa, then the deltas
+    float* const dl = xs;
     __shared__ float sc[LORA_TOK];
     const int t0 = blockIdx.y * LORA_TOK, o0 = blockIdx.x * ROWS;
     const int tn = min(LORA_TOK, a.n - t0);
-    const int half = a.rows / 2, j = threadIdx.x % (ROWS / 2), tp = threadIdx.x / (ROWS / 2);
+    const int half = a.rows / 2, j = 4 * (threadIdx.x % OQ), tp = threadIdx.x / OQ;
     const int rg = 16 * (j >> 3) + (j & 7), og = o0 + rg < a.rows ? o0 + rg : a.rows - 16;  // in bounds
     LoraTiles<R, WT> tiles;
     tiles.load(a, o0);
-    float g[TPT], u[TPT];
+    float4 g[TPT], u[TPT];
 #pragma unroll
     for (int k = 0; k < TPT; k++) {
-        const int t = tp + TS * k;
-        const float* yr = y + (size_t)(t0 + min(t, tn - 1)) * a.ldy + og;
-        g[k] = yr[0];
-        u[k] = yr[8];
+        const float* yr = y + (size_t)(t0 + min(tp + TS * k, tn - 1)) * a.ldy + og;
+        g[k] = *(const float4*)yr;
+        u[k] = *(const float4*)(yr + 8);
     }
     lora_stage_xs(a, t0, xs, sc);
     const int off[2] = {a.tab[4], a.tab[5]};
-    tiles.deltas(a, o0, tn, xs, off, [](int r) { return (r >> 3) & 1; }, dl);
+    tiles.deltas(a, o0, xs, off, [](int r) { return (r >> 3) & 1; }, dl);
     if (o0 + rg >= a.rows) return;
 #pragma unroll
     for (int k = 0; k < TPT; k++) {
         const int t = tp + TS * k;
         if (t >= tn) break;
-        const float gg = g[k] + dl[t * DL_LD + rg], uu = u[k] + dl[t * DL_LD + rg + 8];
-        mid[(size_t)(t0 + t) * half + o0 / 2 + j] = (__bf16)(gg / (1.0f + __expf(-gg)) * uu);
+        const float4 dg = *(const float4*)(dl + t * DL_LD + rg), du = *(const float4*)(dl + t * DL_LD + rg + 8);
+        const float gg[4] = {g[k].x + dg.x, g[k].y + dg.y, g[k].z + dg.z, g[k].w + dg.w};
+        const float uu[4] = {u[k].x + du.x, u[k].y + du.y, u[k].z + du.z, u[k].w + du.w};
+        uint32_t w[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const float lo = gg[2 * i] / (1.0f + __expf(-gg[2 * i])) * uu[2 * i];
+            const float hi = gg[2 * i + 1] / (1.0f + __expf(-gg[2 * i + 1])) * uu[2 * i + 1];
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+        }
+        *(uint2*)(mid + (size_t)(t0 + t) * half + o0 / 2 + j) = uint2{w[0], w[1]};
     }
 }
 
@@ -376,9 +405,10 @@ int lora_check(const float* xa, int split, int m_cols, const uint16_t* b, size_t
         return fail(QH_EINVAL, "lora: null or %d splits", split);
     if (m_cols < 1 || m_cols > LORA_COLS_MAX)
         return fail(QH_EINVAL, "lora: %d columns of xa (at most %d)", m_cols, LORA_COLS_MAX);
-    if (rows == 0 || rows % 16 || rows > (1u << 30) || n > (1u << 24) || ldy < rows || ldy > (1u << 30) ||
-        (uintptr_t)b % 16)
-        return fail(QH_EINVAL, "lora: %zu rows (ld %zu), %zu tokens: rows a multiple of 16, B 16-byte aligned", rows,
+    if (rows == 0 || rows % 16 || rows > (1u << 30) || n > (1u << 24) || ldy < rows || ldy > (1u << 30) || ldy % 4 ||
+        (uintptr_t)b % 16 || (uintptr_t)y % 16)
+        return fail(QH_EINVAL,
+                    "lora: %zu rows (ld %zu), %zu tokens: rows a multiple of 16, ld of 4, B and y 16-byte aligned", rows,
                     ldy, n);
     return QH_OK;
 }
@@ -398,7 +428,7 @@ extern "C" int qh_lora_silu(void* stream, const float* xa, int split, int m_cols
                             size_t rows, const int32_t* tab, const int32_t* tok_slot, const float* slot_scale,
                             size_t n, const float* y, size_t ldy, void* mid_bf16) {
     if (n == 0) return QH_OK;
-    if (!mid_bf16) return fail(QH_EINVAL, "lora silu: null output");
+    if (!mid_bf16 || (uintptr_t)mid_bf16 % 8) return fail(QH_EINVAL, "lora silu: null or unaligned output (8 bytes)");
     if (int e = lora_check(xa, split, m_cols, b_f16, rows, tab, tok_slot, slot_scale, n, y, ldy)) return e;
     const LoraArgs a{xa, split, m_cols, b_f16, rank, (int)rows, tab, tok_slot, slot_scale, (int)n, (int)ldy};
     return lora_launch(stream, a, nullptr, y, (__bf16*)mid_bf16);

@@ -153,3 +153,9 @@ def test_lora_rejects(gemm):
         lora_add(None, z, 1, 512, b, 8, 16, t, t, z, 1, z)
     with pytest.raises(QhError):  # SwiGLU rows not in whole tiles
         lora_silu(None, z, 1, 16, b, 8, 24, t, t, z, 1, z, z)
+    with pytest.raises(QhError):  # y rows not 16-byte aligned (ldy 18)
+        lora_add(None, z, 1, 16, b, 8, 16, t, t, z, 1, z, ldy=18)
+    with pytest.raises(QhError):  # y not 16-byte aligned
+        lora_add(None, z, 1, 16, b, 8, 16, t, t, z, 1, z[1:])
+    with pytest.raises(QhError):  # mid not 8-byte aligned
+        lora_silu(None, z, 1, 16, b, 8, 16, t, t, z, 1, z, z.view(torch.int16)[1:])
