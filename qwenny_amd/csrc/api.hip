@@ -291,7 +291,8 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
         const int wt = std::max(1, std::min({want_wt, cols, tokens > 16 ? 8 : 16}));
         // QH_SKINNY_PLAIN_WK (tuning): wave rows over K within the workgroup, dividing the partials
         const int pk = ctx->skinny_plain_wk;
-        if (pk > 1 && (G / ng) % pk == 0 && wt * pk <= 16) return Partition{wt, wt * pk, G / ng / pk, ng};
+        if (pk > 1 && (G / ng) % pk == 0 && wt * pk <= (tokens > 16 ? 8 : 16))
+            return Partition{wt, wt * pk, G / ng / pk, ng};
         return Partition{wt, wt, G / ng, ng};
     }
     const size_t per_group = std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's activations
@@ -354,7 +355,7 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
         l.groups_per_wave = p.groups_per_wave;
         // 16-byte row runs need a 16-byte aligned y (its rows are: the row count is a multiple of 16)
         // (one token: the LDS round trip costs more than it saves, measured 3% on small matrices)
-        l.stage_out = epi == QH_EPI_PLAIN && m > 1 && ((uintptr_t)y & 15) == 0 && p.waves == p.tile_waves;
+        l.stage_out = epi == QH_EPI_PLAIN && m > 1 && ((uintptr_t)y & 15) == 0;
     } else {
         l.tile_waves = 4;
         l.waves = 4;

@@ -517,26 +517,30 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
 #pragma unroll
         for (int r = 0; r < NR; r++) key[b][r] = 0;
     if (EPI == EPI_PLAIN && a.stage_out) {
+        if (WK > 1) __syncthreads();  // every lead wave has read the K-wave partials that the staging overwrites
         // plain partials through LDS: the wave's block (m tokens x T 16-row tiles) is written to its own LDS slot in
         // the MFMA layout and read back along the rows, so that y is written with 16-byte stores of whole row runs
         // (one store instruction for up to 8 tokens, against one per tile and token row of 16 lanes: small scattered
         // stores cost far more per byte than the reads they follow)
         constexpr int RW = T * TILE;  // rows of the wave's block
-        float* stg = red + (size_t)wave * M * RW;
+        float* stg = red + (size_t)wt * M * RW;  // the lead wave of tile column wt
+        if (lead) {
 #pragma unroll
-        for (int t = 0; t < T; t++)
+            for (int t = 0; t < T; t++)
 #pragma unroll
-            for (int b = 0; b < TB; b++)
+                for (int b = 0; b < TB; b++)
 #pragma unroll
-                for (int r = 0; r < NR; r++) {
-                    const int tok = 16 * b + 4 * kq + r;
-                    if (tok < M) stg[tok * RW + t * TILE + l16] = acc[b][t][r];
-                }
-        const int row0 = tile0 * TILE;
-        for (int i = lane; i < M * (RW / 4); i += 64) {
-            const int tok = i / (RW / 4), c = 4 * (i - tok * (RW / 4));
-            if (row0 + c < a.rows)
-                *(f32x4*)((float*)a.y + ((size_t)sp * M + tok) * a.ldy + row0 + c) = *(const f32x4*)(stg + tok * RW + c);
+                    for (int r = 0; r < NR; r++) {
+                        const int tok = 16 * b + 4 * kq + r;
+                        if (tok < M) stg[tok * RW + t * TILE + l16] = acc[b][t][r];
+                    }
+            const int row0 = tile0 * TILE;
+            for (int i = lane; i < M * (RW / 4); i += 64) {
+                const int tok = i / (RW / 4), c = 4 * (i - tok * (RW / 4));
+                if (row0 + c < a.rows)
+                    *(f32x4*)((float*)a.y + ((size_t)sp * M + tok) * a.ldy + row0 + c) =
+                        *(const f32x4*)(stg + tok * RW + c);
+            }
         }
     } else if (lead) {
 #pragma unroll
@@ -960,6 +964,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
 
 template <int F, int EPI, int NR, int NG, int TB>
 static hipError_t skinny_ng(const Launch& l) {
+    if (64 * l.waves > (TB == 1 ? 1024 : 512)) return hipErrorInvalidConfiguration;  // the kernel's launch bound
     const int tiles = l.rows / TILE;
     const int per_wg = SKINNY_TILES * l.tile_waves;
     dim3 grid((tiles + per_wg - 1) / per_wg, l.split);
@@ -1128,8 +1133,8 @@ size_t skinny_lds(const Launch& l) {
     const int wk = l.waves / l.tile_waves, tb = (l.m + 15) / 16;
     const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
     const size_t red = (size_t)(wk - 1) * l.tile_waves * tb * SKINNY_TILES * 4 * 64 * sizeof(float);
-    // plain partials staged per wave: m tokens x SKINNY_TILES tiles of f32
-    const size_t out = l.stage_out ? (size_t)l.waves * l.m * SKINNY_TILES * TILE * sizeof(float) : 0;
+    // plain partials staged per tile column's lead wave: m tokens x SKINNY_TILES tiles of f32
+    const size_t out = l.stage_out ? (size_t)l.tile_waves * l.m * SKINNY_TILES * TILE * sizeof(float) : 0;
     return x + std::max(red, out);
 }
 
