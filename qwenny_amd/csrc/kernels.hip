@@ -606,7 +606,8 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
 // An item cut between workgroups is finished by the last of them to arrive: each writes its partial accumulators to
 // its own slot of a scratch buffer (device-coherent stores), then counts itself on the item's counter (a returning
 // device-scope atomic); the one that counts last adds the partials in segment order (so the sum does not depend on
-// who arrives last), runs the epilogue and clears the counter. No workgroup ever waits for another.
+// who arrives last; its own share from its registers when it is the item's first segment, the usual case), runs the
+// epilogue and clears the counter. No workgroup ever waits for another.
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
@@ -930,10 +931,15 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
                                                  __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(sb - sa);
             __syncthreads();
             if (!sk_last) continue;  // uniform over the workgroup
-            // the last segment to arrive: sum the partials in segment order (its own read back like the others, so
-            // that the sum does not depend on the order of arrival), 16 registers at a time
-            clear();
-            for (int o = sa; o <= sb; o++) {
+            // the last segment to arrive: the sum of all segments' partials in segment order from zero (so that it does
+            // not depend on the order of arrival), 16 registers at a time. When it is the item's first segment (the
+            // usual case: it reached the item at the end of its range), its own share, the sum's first term, stays in
+            // its registers; otherwise it reads its own back like the others. Each addition is followed by + 0, which
+            // gives the sum from zero exactly in both cases: (0 + a) + b = (a + b) + 0 for all a, b, and no later sum
+            // from zero is -0 (x + (-x) is +0), so the further + 0 change nothing.
+            const bool own_first = s == sa;
+            if (!own_first) clear();
+            for (int o = own_first ? sa + 1 : sa; o <= sb; o++) {
                 const uint32_t src = sk_off(2 * o + (sk_begin(o, a.sk_q, a.sk_r) < su), wave, lane);
 #pragma unroll
                 for (int q0 = 0; q0 < NQ; q0 += SK_QC) {
@@ -946,7 +952,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
                     for (int i = 0; i < SK_QC; i++) {
                         const int q = q0 + i, e = (q & 3) * 4;
                         f32x16& d = acc[(q >> 2) / TN][(q >> 2) % TN];
-                        d[e] += v[i][0], d[e + 1] += v[i][1], d[e + 2] += v[i][2], d[e + 3] += v[i][3];
+#pragma unroll
+                        for (int c = 0; c < 4; c++) d[e + c] = (d[e + c] + v[i][c]) + 0.0f;
                     }
                     __builtin_amdgcn_sched_barrier(0);  // one chunk of loads in flight at a time (registers)
                 }
