@@ -130,28 +130,28 @@ __device__ __forceinline__ void argmax_spread_max(const Launch& a, int tok, unsi
                                  __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ void argmax_finish(const Launch& a) {
+__device__ void argmax_finish(const Launch& a, int tid, int nthr) {
     __shared__ int last;
     __shared__ unsigned long long best[ARGMAX_MAX_TOK];
     __builtin_amdgcn_s_waitcnt(0);  // this wave's table updates have returned
     __syncthreads();
-    if (threadIdx.x == 0)
+    if (tid == 0)
         last = __hip_atomic_fetch_add(a.argmax_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                gridDim.x * gridDim.y - 1;
-    for (int t = threadIdx.x; t < a.m; t += blockDim.x) best[t] = 0;
+    for (int t = tid; t < a.m; t += nthr) best[t] = 0;
     __syncthreads();
     if (!last) return;  // uniform over the workgroup
-    for (int i = threadIdx.x; i < ARGMAX_SPREAD * a.m; i += blockDim.x) {
+    for (int i = tid; i < ARGMAX_SPREAD * a.m; i += nthr) {
         const int row = i / a.m, tok = i - row * a.m;
         const unsigned long long k = __hip_atomic_exchange(a.argmax_table + row * ARGMAX_MAX_TOK + tok, 0ull,
                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (k) atomicMax(best + tok, k);
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < a.m; t += blockDim.x)
+    for (int t = tid; t < a.m; t += nthr)
         if (best[t])
             (void)__hip_atomic_fetch_max(a.keys + t, best[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0)
+    if (tid == 0)
         (void)__hip_atomic_exchange(a.argmax_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -308,12 +308,26 @@ template <int F, int EPI, int NR, int T, int NG, int TB>
 __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int CW = CodeWords<F>::N;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nthr = blockDim.x, WT = a.tile_waves, WK = (nthr >> 6) / WT, wt = wave % WT, wk = wave / WT;
+    // the workgroup is WT wave columns (x) by WK wave rows (y): no division in the index set-up, which every wave
+    // runs before its first load
+    const int lane = threadIdx.x & 63, nthr = blockDim.x * blockDim.y, tid = threadIdx.y * blockDim.x + threadIdx.x;
+    const int WT = blockDim.x >> 6, WK = blockDim.y;
+    const int wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wk = __builtin_amdgcn_readfirstlane(threadIdx.y);
     const int l16 = lane & 15, kq = lane >> 4;
     const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
-    const int CH = WK * NG, NC = G / CH;  // groups per super-chunk, super-chunks in K
-    const int c0 = (int)((long)blockIdx.y * NC / a.split), c1 = (int)((long)(blockIdx.y + 1) * NC / a.split);
+    const int CH = WK * NG, NC = a.nc;  // groups per super-chunk, super-chunks in K
+    // super-chunks [c0, c1) of this split: one each (plain products), all (split 1), else an even share
+    int c0, c1;
+    if (a.split == NC) {
+        c0 = blockIdx.y;
+        c1 = c0 + 1;
+    } else if (a.split == 1) {
+        c0 = 0;
+        c1 = NC;
+    } else {
+        c0 = (int)(blockIdx.y * (unsigned)NC / (unsigned)a.split);
+        c1 = (int)((blockIdx.y + 1) * (unsigned)NC / (unsigned)a.split);
+    }
     const int tile0 = (blockIdx.x * WT + wt) * T;
     const int xpitch = CH * QG + 8;  // bf16 per staged x row (+16 bytes: rows start 4 banks apart)
     __bf16* xs_lds = (__bf16*)smem;
@@ -354,7 +368,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
         int xo[XPT];
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
-            const int p = threadIdx.x + i * nthr;
+            const int p = tid + i * nthr;
             const int tok = min(p / rowc, M - 1), pc = p - (p / rowc) * rowc;
             xo[i] = p < npieces ? tok * xpitch + 8 * pc : -1;
             xv[i] = *(const u32x4*)((const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx +
@@ -393,7 +407,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
 #pragma unroll
         for (int i = 0; i < XPT; i++)
             if (xo[i] >= 0) *(u32x4*)(xs_lds + xo[i]) = xv[i];
-        for (int p = threadIdx.x + XPT * nthr; p < npieces; p += nthr) {
+        for (int p = tid + XPT * nthr; p < npieces; p += nthr) {
             const int tok = p / rowc, pc = p - tok * rowc;
             const __bf16* src =
                 (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
@@ -575,7 +589,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
                 const int tok = 16 * b + 4 * kq + r;
                 if (lead && l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
             }
-        argmax_finish(a);
+        argmax_finish(a, tid, nthr);
     }
 }
 
@@ -963,7 +977,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         }
         epilogue();
     }
-    if (EPI == EPI_ARGMAX) argmax_finish(a);
+    if (EPI == EPI_ARGMAX) argmax_finish(a, threadIdx.x, blockDim.x);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -975,8 +989,11 @@ static hipError_t skinny_ng(const Launch& l) {
     const int tiles = l.rows / TILE;
     const int per_wg = SKINNY_TILES * l.tile_waves;
     dim3 grid((tiles + per_wg - 1) / per_wg, l.split);
-    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.waves), skinny_lds(l),
-                       l.stream, l);
+    Launch k = l;
+    const int wk = l.waves / l.tile_waves;
+    k.nc = l.cols / QG / (wk * NG);
+    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.tile_waves, wk),
+                       skinny_lds(l), l.stream, k);
     return hipGetLastError();
 }
 
