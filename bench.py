@@ -622,7 +622,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of lines: m1,m5,prefill,pfzp,pfshort,int8,i8g,dense,dequant,set4b,c0,consumers,"
+                    help="comma list of lines: m1,m1sum,m5,prefill,pfzp,pfshort,int8,i8g,dense,dequant,set4b,c0,consumers,"
                          "lora")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
@@ -666,7 +666,7 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"set4b_run": "done"}))
         return
-    only = set(args.only.split(",")) if args.only else {"m1", "m5", "prefill", "pfzp", "pfshort", "int8", "i8g", "dense",
+    only = set(args.only.split(",")) if args.only else {"m1", "m1sum", "m5", "prefill", "pfzp", "pfshort", "int8", "i8g", "dense",
                                                          "dequant", "set4b", "c0", "consumers", "lora"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
@@ -720,6 +720,30 @@ def main():
           f"{per_launch_bytes / per_launch_s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 
     extra = {}
+    if "m1sum" in only:
+        # the same step with each plain product's split-K partials summed (sum_parts, one launch after each): what a
+        # caller that needs whole rows pays on top of the products, over the same algorithmic bytes
+        sst = decode_step(1)
+        sums = {}
+
+        def run_with_sums(stream=None):
+            from qwenny_amd import sum_parts
+
+            for mat, epi, y, _, _ in sst.launches:
+                if epi == Epi.Argmax:
+                    gemm.run(stream, 1, mat, sst.x, y, epi, n_out=1, keys=sst.keys)
+                    continue
+                split = gemm.run(stream, 1, mat, sst.x, y, epi)
+                key = mat.rows
+                if key not in sums:
+                    sums[key] = torch.empty(mat.rows, dtype=torch.float32, device="cuda")
+                sum_parts(stream, y, split, 1, mat.rows, sums[key])
+
+        sst.run = run_with_sums
+        sms = time_step(sst, args.steps, args.warmup, not args.no_graph)
+        extra["m1_with_sums"] = {"GBps": round(sst.bytes() / (sms * 1e-3) / 1e9, 1), "ms_per_step": round(sms, 5)}
+        print(f"# M=1 27B set x4 + head, each plain product's partials summed: {sms:.4f} ms/step, "
+              f"{sst.bytes() / (sms * 1e-3) / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
     if "m5" in only:
         st5 = decode_step(5)
         ms5 = time_step(st5, args.steps, args.warmup, not args.no_graph)
