@@ -179,8 +179,8 @@ __device__ __forceinline__ int zero_of(const uint16_t* zeros, int tile, int G, i
 //
 // A wave owns T tiles and NG consecutive groups (one "chunk"): it issues all of that chunk's loads at once (its
 // scales, one load per tile for 4 groups, then the codes), so that many short waves keep HBM saturated, and computes
-// them as they arrive. The workgroup's waves are WT side by side over tiles times WK over consecutive chunks of K;
-// together they cover a super-chunk of CH = WK * NG groups, whose activations the workgroup stages once in LDS
+// them as they arrive. The workgroup's waves are WT side by side over tiles (x) times WK over consecutive chunks of K
+// (y); together they cover a super-chunk of CH = WK * NG groups, whose activations the workgroup stages once in LDS
 // (every wave of it reads them with ds_read_b128 instead of fetching them from L2). The grid's y dimension splits the
 // super-chunks of K (plain products: split-K partials); WK waves' partial sums are reduced through LDS.
 
