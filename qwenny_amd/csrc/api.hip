@@ -165,7 +165,7 @@ extern "C" int qh_mat_upload(qh_ctx* ctx, int wt, size_t rows, size_t cols, cons
         for (size_t t = 0; t < tiles && m->per_channel; t++)
             for (int r = 0; r < TILE && m->per_channel; r++)
                 for (size_t g = 1; g < G && m->per_channel; g++)
-                    m->per_channel = s[scale_idx(t, G, g, r)] == s[scale_idx(t, G, 0, r)];
+                    m->per_channel = s[scale_idx(t, tiles, g, r)] == s[scale_idx(t, tiles, 0, r)];
     }
     *out = m;
     return QH_OK;
@@ -460,8 +460,11 @@ extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant
                 if (zeros[rows16[r] * qgroups + g] != 8)
                     return fail(QH_EINVAL, "rows with zero points for a symmetric matrix");
     }
-    const size_t tiles = m->rows / TILE;
+    // one tile's codes are contiguous; its scales and zero points are one run per quad of 4 groups, a quad's tiles
+    // side by side (layout.h), so they go as strided copies
+    const size_t tiles = m->rows / TILE, nq = quads(m->cols / QG);
     const size_t cb = m->code_bytes / tiles, sb = m->scale_bytes / tiles, zb = m->zero_bytes / tiles;
+    const size_t sq = sb / nq, zq = zb / nq;  // bytes of one tile's run in one quad
     HIP_TRY(hipEventSynchronize(m->staged));  // the previous block's copies have left the staging buffer
     uint8_t* st = m->stage;
     if (!f32_scales(m->wt))
@@ -475,8 +478,12 @@ extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant
         return e;
     hipStream_t s = (hipStream_t)stream;
     HIP_TRY(hipMemcpyAsync((uint8_t*)m->codes + block * cb, st, cb, hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync((uint8_t*)m->scales + block * sb, st + cb, sb, hipMemcpyHostToDevice, s));
-    if (zb) HIP_TRY(hipMemcpyAsync((uint8_t*)m->zeros + block * zb, st + cb + sb, zb, hipMemcpyHostToDevice, s));
+    // the staged tile was packed alone (one tile: its quads' runs are consecutive)
+    HIP_TRY(hipMemcpy2DAsync((uint8_t*)m->scales + block * sq, tiles * sq, st + cb, sq, sq, nq, hipMemcpyHostToDevice,
+                             s));
+    if (zb)
+        HIP_TRY(hipMemcpy2DAsync((uint8_t*)m->zeros + block * zq, tiles * zq, st + cb + sb, zq, zq, nq,
+                                 hipMemcpyHostToDevice, s));
     HIP_TRY(hipEventRecord(m->staged, s));
     m->valid = std::max(m->valid, (block + 1) * TILE);
     return QH_OK;

@@ -177,7 +177,7 @@ extern "C" int qh_packed_sizes(int wt, size_t rows, size_t cols, size_t* code_by
 // k .. k + 32 / bits - 1 of `row` in the checkpoint's order (value c at bits c * bits); scale(row, g), zero(row, g) per
 // 128-column group.
 template <class Word, class Scale, class Zero>
-static void pack_tile(int wt, size_t cols, const size_t* rows16, size_t t, Word word, Scale scale, Zero zero,
+static void pack_tile(int wt, size_t cols, const size_t* rows16, size_t t, size_t T, Word word, Scale scale, Zero zero,
                       void* codes, void* scales, void* zeros) {
     const size_t G = cols / QG;
     for (size_t g = 0; g < G; g++) {
@@ -205,16 +205,16 @@ static void pack_tile(int wt, size_t cols, const size_t* rows16, size_t t, Word 
         for (int r = 0; r < TILE; r++) {
             const float sc = g < G ? scale(rows16[r], g) : 0.0f;
             if (f32_scales(wt))
-                ((float*)scales)[scale_idx(t, G, g, r)] = sc;
+                ((float*)scales)[scale_idx(t, T, g, r)] = sc;
             else
-                ((uint16_t*)scales)[scale_idx(t, G, g, r)] = f32_to_bf16(sc);
+                ((uint16_t*)scales)[scale_idx(t, T, g, r)] = f32_to_bf16(sc);
         }
     if (has_zeros(wt))
         for (size_t q4 = 0; q4 < quads(G); q4++)
             for (int r = 0; r < TILE; r++) {
                 uint16_t z = 0;
                 for (size_t g = 4 * q4; g < std::min(G, 4 * q4 + 4); g++) z |= (uint16_t)((zero(rows16[r], g) & 15u) << (4 * (g % 4)));
-                ((uint16_t*)zeros)[zero_idx(t, G, 4 * q4, r)] = z;
+                ((uint16_t*)zeros)[zero_idx(t, T, 4 * q4, r)] = z;
             }
 }
 
@@ -237,7 +237,7 @@ extern "C" int qh_pack_quant(const qh_quant* q, const uint8_t* zeros, const size
     auto zero = [&](size_t row, size_t g) -> uint32_t { return zeros ? zeros[row * qgroups + g / gstep] : 8; };
     parallel(n / TILE, [&](size_t lo, size_t hi) {
         for (size_t t = lo; t < hi; t++)
-            pack_tile(wt, q->cols, order + t * TILE, t, word, scale, zero, codes, scales, zeros_out);
+            pack_tile(wt, q->cols, order + t * TILE, t, n / TILE, word, scale, zero, codes, scales, zeros_out);
     });
     return QH_OK;
 }
@@ -248,7 +248,7 @@ extern "C" int qh_unpack_row(int wt, size_t rows, size_t cols, const void* codes
     if (is_bf16(wt)) return fail(QH_EINVAL, "unpack: dense bf16 rows unpack with qh_unpack_row_bf16");
     if (p >= rows || !codes || !scales || !vals || !sc || !z || (has_zeros(wt) && !zeros))
         return fail(QH_EINVAL, "unpack: row %zu of %zu or null buffer", p, rows);
-    size_t G = cols / QG, t = p / TILE;
+    size_t G = cols / QG, t = p / TILE, T = rows / TILE;
     int r = (int)(p % TILE);
     for (size_t g = 0; g < G; g++) {
         size_t blk = t * G + g;
@@ -270,10 +270,10 @@ extern "C" int qh_unpack_row(int wt, size_t rows, size_t cols, const void* codes
                 }
             }
         }
-        sc[g] = f32_scales(wt) ? ((const float*)scales)[scale_idx(t, G, g, r)]
-                               : bf16_to_f32(((const uint16_t*)scales)[scale_idx(t, G, g, r)]);
+        sc[g] = f32_scales(wt) ? ((const float*)scales)[scale_idx(t, T, g, r)]
+                               : bf16_to_f32(((const uint16_t*)scales)[scale_idx(t, T, g, r)]);
         z[g] = is_i8(wt)       ? 128
-               : has_zeros(wt) ? (uint8_t)((((const uint16_t*)zeros)[zero_idx(t, G, g, r)] >> (4 * (g % 4))) & 15u)
+               : has_zeros(wt) ? (uint8_t)((((const uint16_t*)zeros)[zero_idx(t, T, g, r)] >> (4 * (g % 4))) & 15u)
                                : 8;
     }
     return QH_OK;
@@ -314,7 +314,7 @@ extern "C" int qh_pack_dense_int8(const uint16_t* bf16, size_t rows, size_t cols
             auto word = [&](size_t r, size_t k) { return qw[(r * cols + k) / 4]; };
             auto scale = [&](size_t r, size_t g) { return sc[r * G + g]; };
             auto zero = [](size_t, size_t) -> uint32_t { return 128; };
-            pack_tile(QH_WT_I8, cols, local, t, word, scale, zero, codes, scales, nullptr);
+            pack_tile(QH_WT_I8, cols, local, t, n / TILE, word, scale, zero, codes, scales, nullptr);
         }
     });
     return QH_OK;

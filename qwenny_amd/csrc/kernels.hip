@@ -161,17 +161,11 @@ struct CodeWords {
     static constexpr int N = (F & F_BF16) ? 4 : (F & F_I8) ? 2 : 1;
 };
 
-// The scale and zero point of row r of `tile`, group g (G groups; layout.h scale_idx / zero_idx)
+// The scale of row r of `tile`, group g (T tiles; layout.h scale_idx)
 template <int F>
-__device__ __forceinline__ float scale_of(const void* scales, int tile, int G, int g, int r) {
-    if (F & F_S32) return ((const float*)scales)[scale_idx(tile, G, g, r)];
-    return bf16_bits_f(((const uint16_t*)scales)[scale_idx(tile, G, g, r)]);
-}
-
-template <int F>
-__device__ __forceinline__ int zero_of(const uint16_t* zeros, int tile, int G, int g, int r) {
-    if (F & F_ZP) return (int)((zeros[zero_idx(tile, G, g, r)] >> (4 * (g & 3))) & 15u);
-    return (F & F_I8) ? 128 : 8;
+__device__ __forceinline__ float scale_of(const void* scales, int tile, int T, int g, int r) {
+    if (F & F_S32) return ((const float*)scales)[scale_idx(tile, T, g, r)];
+    return bf16_bits_f(((const uint16_t*)scales)[scale_idx(tile, T, g, r)]);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -380,7 +374,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
         u32x4 code[NG][T][CW];
 #pragma unroll
         for (int t = 0; t < T && !(F & F_BF16); t++) {
-            const size_t si = scale_idx(tt[t], G, gw, l16);
+            const size_t si = scale_idx(tt[t], tiles, gw, l16);
             if constexpr (NG == 4) {
                 if constexpr ((F & F_S32) != 0) {
                     const u32x4 v = *(const u32x4*)((const float*)a.scales + si);
@@ -392,7 +386,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
             } else {
                 sraw[t][0] = (F & F_S32) ? ((const uint32_t*)a.scales)[si] : ((const uint16_t*)a.scales)[si];
             }
-            if (F & F_ZP) zraw[t] = a.zeros[zero_idx(tt[t], G, gw, l16)];
+            if (F & F_ZP) zraw[t] = a.zeros[zero_idx(tt[t], tiles, gw, l16)];
         }
 #pragma unroll
         for (int gi = 0; gi < NG; gi++)
@@ -705,8 +699,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         for (int t = 0; t < TN; t++) {
             tt[t] = min(tile0 + 2 * t + (l32 >> 4), tiles - 1);
             cg[t] = (uint32_t)(((size_t)tt[t] * G * 64 * CW + 16 * lh + l16) * 16);
-            sg[t] = (uint32_t)(scale_idx(tt[t], G, 0, l16) * ((F & F_S32) ? 4 : 2));
-            zg[t] = (uint32_t)(zero_idx(tt[t], G, 0, l16) * 2);
+            sg[t] = (uint32_t)(scale_idx(tt[t], tiles, 0, l16) * ((F & F_S32) ? 4 : 2));
+            zg[t] = (uint32_t)(zero_idx(tt[t], tiles, 0, l16) * 2);
         }
     };
     struct WFrag {
@@ -715,7 +709,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     };
     auto wload = [&](int g, WFrag& f) {
         const uint8_t* cb = (const uint8_t*)a.codes + (size_t)g * 64 * CW * 16;
-        const size_t sq = ((size_t)(g >> 2) * TILE * 4 + (g & 3)) * ((F & F_S32) ? 4 : 2);
+        const size_t sq = ((size_t)(g >> 2) * tiles * TILE * 4 + (g & 3)) * ((F & F_S32) ? 4 : 2);
 #pragma unroll
         for (int t = 0; t < TN; t++) {
 #pragma unroll
@@ -733,7 +727,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
                 f.s[t] = (F & F_S32) ? *(const float*)sp : bf16_bits_f(*(const uint16_t*)sp);
                 int z = (F & F_I8) ? 128 : 8;
                 if (F & F_ZP)
-                    z = (*(const uint16_t*)((const uint8_t*)a.zeros + (size_t)(g >> 2) * TILE * 2 + zg[t]) >>
+                    z = (*(const uint16_t*)((const uint8_t*)a.zeros + (size_t)(g >> 2) * tiles * TILE * 2 + zg[t]) >>
                          (4 * (g & 3))) & 15;
                 f.off[t] = -(float)z * f.s[t];
             }
@@ -831,7 +825,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         if (F & F_PERCH) {  // the row's scale after the exact integer sum
 #pragma unroll
             for (int t = 0; t < TN; t++) {
-                const float rs = scale_of<F>(a.scales, tt[t], G, 0, l16);
+                const float rs = scale_of<F>(a.scales, tt[t], tiles, 0, l16);
 #pragma unroll
                 for (int bb = 0; bb < BMB; bb++)
 #pragma unroll

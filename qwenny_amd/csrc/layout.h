@@ -18,11 +18,12 @@
 //  bf16 (QH_WT_BF16, dense 16-bit weights): 4096 B per block = [j][lane] 16 bytes, the lane's 8 columns of step j as
 //    bf16 in column order, so that each 16-byte piece is a B fragment as loaded. No scales or zero points.
 //
-// Scales: per tile, per quad of 4 groups (the group count padded up to a multiple of 4), per row of the tile, the
-// quad's 4 groups: [t][g / 4][16][g % 4], so that one 8-byte load gives a row the scales of 4 consecutive groups.
-// bf16 for int4 (exact for bf16-stored checkpoint scales), f32 for int8 and for the int4 _S32 storages (scales bf16
-// does not hold exactly).
-// Zero points (QH_WT_I4Z, QH_WT_I4Z_S32): [t][g / 4][16] u16, nibble g % 4 = the zero point of that row and group.
+// Scales: per quad of 4 groups (the group count padded up to a multiple of 4), per tile, per row of the tile, the
+// quad's 4 groups: [g / 4][t][16][g % 4] (T tiles), so that one 8-byte load gives a row the scales of 4 consecutive
+// groups, and the tiles of one quad, which the decode kernel's concurrently running workgroups read together, are one
+// contiguous run. bf16 for int4 (exact for bf16-stored checkpoint scales), f32 for int8 and for the int4 _S32
+// storages (scales bf16 does not hold exactly).
+// Zero points (QH_WT_I4Z, QH_WT_I4Z_S32): [g / 4][t][16] u16, nibble g % 4 = the zero point of that row and group.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -46,12 +47,12 @@ constexpr size_t block_bytes(int wt) { return is_bf16(wt) ? 4096 : is_i8(wt) ? 2
 
 // quads of 4 groups (scale and zero-point blocks) for G groups
 constexpr size_t quads(size_t G) { return (G + 3) / 4; }
-// element index of the scale of tile t, group g, row r (G groups in the matrix)
-constexpr size_t scale_idx(size_t t, size_t G, size_t g, int r) {
-    return ((t * quads(G) + g / 4) * TILE + (size_t)r) * 4 + g % 4;
+// element index of the scale of tile t, group g, row r (T tiles in the matrix)
+constexpr size_t scale_idx(size_t t, size_t T, size_t g, int r) {
+    return (((g / 4) * T + t) * TILE + (size_t)r) * 4 + g % 4;
 }
-// u16 index of the zero-point nibbles of tile t, quad g / 4, row r
-constexpr size_t zero_idx(size_t t, size_t G, size_t g, int r) { return (t * quads(G) + g / 4) * TILE + (size_t)r; }
+// u16 index of the zero-point nibbles of tile t, quad g / 4, row r (T tiles)
+constexpr size_t zero_idx(size_t t, size_t T, size_t g, int r) { return ((g / 4) * T + t) * TILE + (size_t)r; }
 
 // nibble position of column c (0..7) inside a packed int4 word
 constexpr int nib_pos(int c) { return (c & 1) ? 4 + (c >> 1) : (c >> 1); }
