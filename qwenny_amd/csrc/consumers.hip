@@ -14,10 +14,12 @@ using namespace qh;
 
 namespace {
 
-// v += x[0][i] + x[1][i] + .. + x[splits - 1][i], in that order; the partials load 8 at a time ahead of their adds
-// (the sum of 34 partials of a decode product is then 5 memory round trips, not 34)
+// v += x[0][i] + x[1][i] + .. + x[splits - 1][i], in that order; the partials load B at a time ahead of their adds
+// (the sum of 34 partials of a decode product is then 3-5 memory round trips, not 34). Decode sizes, where few
+// workgroups each wait on their loads: B = 16 (the 10-12 partials of most decode products in one round trip; 32
+// measured slower); streaming sizes: B = 8.
+template <int B = 8>
 __device__ __forceinline__ void add_splits(float4& v, const float4* __restrict__ x, int splits, long n4, long i) {
-    constexpr int B = 8;
     for (int s0 = 0; s0 < splits; s0 += B) {
         float4 p[B];
 #pragma unroll
@@ -31,11 +33,12 @@ __device__ __forceinline__ void add_splits(float4& v, const float4* __restrict__
 
 // y [n][ld] = sum over s of x [s][n][ld] (from 0; h = nullptr), or h [n][ld] += that sum (h + x[0] first, as the
 // residual step adds); one thread per 4 columns (ld % 4 == 0), grid-stride over n * ld / 4
+template <int B>
 __global__ __launch_bounds__(256) void sum_parts_kernel(const float4* __restrict__ x, int splits, long n4, float4* y,
                                                         float4* h) {
     for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
         float4 v = h ? h[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        add_splits(v, x, splits, n4, i);
+        add_splits<B>(v, x, splits, n4, i);
         (h ? h : y)[i] = v;
     }
 }
@@ -438,8 +441,12 @@ extern "C" int qh_lora_silu(void* stream, const float* xa, int split, int m_cols
 // 4x as many CUs), 256 otherwise
 static int sum_launch(hipStream_t s, const float* x, int splits, long n4, float* y, float* h) {
     const unsigned t = n4 < 64l * 1024 ? 64 : 256, blocks = (unsigned)std::min<long>((n4 + t - 1) / t, 4096);
-    hipLaunchKernelGGL(sum_parts_kernel, dim3(blocks), dim3(t), 0, s, (const float4*)x, splits, n4, (float4*)y,
-                       (float4*)h);
+    if (t == 64)
+        hipLaunchKernelGGL(sum_parts_kernel<16>, dim3(blocks), dim3(t), 0, s, (const float4*)x, splits, n4,
+                           (float4*)y, (float4*)h);
+    else
+        hipLaunchKernelGGL(sum_parts_kernel<8>, dim3(blocks), dim3(t), 0, s, (const float4*)x, splits, n4,
+                           (float4*)y, (float4*)h);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_EHIP;
 }
 
