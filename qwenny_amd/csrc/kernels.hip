@@ -368,7 +368,8 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
             xv[i] = *(const u32x4*)((const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx +
                                     (size_t)gs * QG + 8 * (p < npieces ? pc : 0));
         }
-        // 2. this wave's weights: scales (4 groups per load), zero points, then codes group by group
+        // 2. this wave's weights: scales (4 groups per load), zero points, then codes group by group, all streamed
+        //    (non-temporal: read once; measured 1-2% faster for the scales, 10% for the codes, than cached loads)
         uint32_t sraw[T][NG == 4 ? ((F & F_S32) ? 4 : 2) : 1];
         uint32_t zraw[T];
         u32x4 code[NG][T][CW];
@@ -377,16 +378,18 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
             const size_t si = scale_idx(tt[t], tiles, gw, l16);
             if constexpr (NG == 4) {
                 if constexpr ((F & F_S32) != 0) {
-                    const u32x4 v = *(const u32x4*)((const float*)a.scales + si);
+                    const u32x4 v = __builtin_nontemporal_load((const u32x4*)((const float*)a.scales + si));
                     sraw[t][0] = v.x, sraw[t][1] = v.y, sraw[t][2] = v.z, sraw[t][3] = v.w;
                 } else {
-                    const uint2 v = *(const uint2*)((const uint16_t*)a.scales + si);
-                    sraw[t][0] = v.x, sraw[t][1] = v.y;
+                    const unsigned long long v =
+                        __builtin_nontemporal_load((const unsigned long long*)((const uint16_t*)a.scales + si));
+                    sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
                 }
             } else {
-                sraw[t][0] = (F & F_S32) ? ((const uint32_t*)a.scales)[si] : ((const uint16_t*)a.scales)[si];
+                sraw[t][0] = (F & F_S32) ? __builtin_nontemporal_load((const uint32_t*)a.scales + si)
+                                         : __builtin_nontemporal_load((const uint16_t*)a.scales + si);
             }
-            if (F & F_ZP) zraw[t] = a.zeros[zero_idx(tt[t], tiles, gw, l16)];
+            if (F & F_ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tt[t], tiles, gw, l16));
         }
 #pragma unroll
         for (int gi = 0; gi < NG; gi++)
