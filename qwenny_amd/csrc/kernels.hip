@@ -298,6 +298,15 @@ __device__ void lora_item32(const Launch& a, int tile0, int tok0, f32x16 (&acc)[
     }
 }
 
+// Whether a skinny launch stages the activations per wave instead of per workgroup: one token, int4 without zero
+// points, 4-group waves. Each wave then loads its own 1 KiB of x (from L2: the x reads grow by the workgroup's wave
+// count, against the 8 KiB of weights per wave) and waits for no other wave before it computes. Same-box A/B, per
+// launch: the 27B set 8.00 -> 7.90 us, configs[0] 4.81 -> 4.73 us; with zero points (the 4B set) it measured 3% slower,
+// int8 and bf16 1-2% slower, so those keep the workgroup's staging.
+__host__ __device__ constexpr bool skinny_wave_x(int m, int fmt, int ng) {
+    return m == 1 && ng == 4 && !(fmt & (F_I8 | F_BF16 | F_ZP));
+}
+
 template <int F, int EPI, int NR, int T, int NG, int TB>
 __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -325,7 +334,12 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
     const int tile0 = (blockIdx.x * WT + wt) * T;
     const int xpitch = CH * QG + 8;  // bf16 per staged x row (+16 bytes: rows start 4 banks apart)
     __bf16* xs_lds = (__bf16*)smem;
-    float* red = (float*)(smem + (((size_t)M * xpitch * 2 + 15) & ~(size_t)15));
+    // one token (int4 without zero points, 4-group waves): each wave stages its own groups' activations (1 KiB, one
+    // direct-to-LDS load per lane) in its own LDS slot, and no workgroup barrier separates its loads from its compute
+    constexpr bool PRIV = NR == 1 && TB == 1 && skinny_wave_x(1, F, NG);
+    __bf16* xw = xs_lds + (size_t)(wk * WT + wt) * NG * QG;
+    const size_t xbytes = PRIV ? std::max((size_t)M * xpitch * 2, (size_t)WT * WK * NG * QG * 2) : (size_t)M * xpitch * 2;
+    float* red = (float*)(smem + ((xbytes + 15) & ~(size_t)15));
 
     int tt[T];
 #pragma unroll
@@ -357,9 +371,16 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
         //    the rest, if any, afterwards
         const int rowc = CH * 16;  // 16-byte pieces per row
         const int npieces = M * rowc;
-        constexpr int XPT = TB;  // activation pieces each thread loads ahead of the weights
-        u32x4 xv[XPT];
-        int xo[XPT];
+        constexpr int XPT = PRIV ? 0 : TB;  // activation pieces each thread loads ahead of the weights
+        u32x4 xv[XPT > 0 ? XPT : 1];
+        int xo[XPT > 0 ? XPT : 1];
+        if constexpr (PRIV) {  // the wave's own 4 groups (64 pieces of 16 bytes), global -> LDS directly
+            __builtin_amdgcn_global_load_lds(
+                (const void*)((const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[0] : 0) * a.ldx + (size_t)gw * QG +
+                              8 * lane),
+                (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int p = tid + i * nthr;
@@ -400,17 +421,24 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
                 for (int h = 0; h < CW; h++) code[gi][t][h] = __builtin_nontemporal_load(cp + h * 64 + lane);
             }
         // 3. stage the activations
-        if (c > c0) __syncthreads();  // the previous super-chunk's readers are done
+        if constexpr (PRIV) {
+            // the wave's own activation load done: the weight loads issued after it (a scale load and NG code loads
+            // per tile) may stay in flight. Its previous super-chunk's LDS reads were all consumed by its MFMAs.
+            constexpr int WL = T * (1 + NG * CW);
+            __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
+        } else {
+            if (c > c0) __syncthreads();  // the previous super-chunk's readers are done
 #pragma unroll
-        for (int i = 0; i < XPT; i++)
-            if (xo[i] >= 0) *(u32x4*)(xs_lds + xo[i]) = xv[i];
-        for (int p = tid + XPT * nthr; p < npieces; p += nthr) {
-            const int tok = p / rowc, pc = p - tok * rowc;
-            const __bf16* src =
-                (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
-            *(u32x4*)(xs_lds + (size_t)tok * xpitch + 8 * pc) = *(const u32x4*)src;
+            for (int i = 0; i < XPT; i++)
+                if (xo[i] >= 0) *(u32x4*)(xs_lds + xo[i]) = xv[i];
+            for (int p = tid + XPT * nthr; p < npieces; p += nthr) {
+                const int tok = p / rowc, pc = p - tok * rowc;
+                const __bf16* src =
+                    (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
+                *(u32x4*)(xs_lds + (size_t)tok * xpitch + 8 * pc) = *(const u32x4*)src;
+            }
+            __syncthreads();
         }
-        __syncthreads();
         // 3. compute the wave's groups: each tile's B fragments once, against every token block
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
@@ -418,7 +446,8 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
             f32x4 xsum[TB];
 #pragma unroll
             for (int b = 0; b < TB; b++) {
-                const __bf16* xrow = xs_lds + (size_t)xtok[b] * xpitch + (wk * NG + gi) * QG + 8 * kq;
+                const __bf16* xrow = PRIV ? xw + gi * QG + 8 * kq
+                                          : xs_lds + (size_t)xtok[b] * xpitch + (wk * NG + gi) * QG + 8 * kq;
 #pragma unroll
                 for (int j = 0; j < 4; j++) xa[b][j] = *(const u32x4*)(xrow + 32 * j);
                 xsum[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1152,7 +1181,9 @@ template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(Launch& l);
 #ifdef QH_PART_DISPATCH
 size_t skinny_lds(const Launch& l) {
     const int wk = l.waves / l.tile_waves, tb = (l.m + 15) / 16;
-    const size_t x = ((size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2 + 15) & ~(size_t)15;
+    const size_t x0 = (size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2;  // the workgroup's staged rows
+    const size_t xw = skinny_wave_x(l.m, l.fmt, l.groups_per_wave) ? (size_t)l.waves * l.groups_per_wave * QG * 2 : 0;
+    const size_t x = (std::max(x0, xw) + 15) & ~(size_t)15;
     const size_t red = (size_t)(wk - 1) * l.tile_waves * tb * SKINNY_TILES * 4 * 64 * sizeof(float);
     // plain partials staged per tile column's lead wave: m tokens x SKINNY_TILES tiles of f32
     const size_t out = l.stage_out ? (size_t)l.tile_waves * l.m * SKINNY_TILES * TILE * sizeof(float) : 0;
