@@ -686,6 +686,10 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // two objects, so that the compiler can tell the direct-to-LDS loads into one from the reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
+    // the ping-pong schedule (below) keeps a whole group's two stages and the next group's in flight: two more
+    constexpr bool PP = NW == 8 && WM == 1 && TN == 1 && !(F & F_ZP) && !LORA;
+    __shared__ __attribute__((aligned(PP ? 1024 : 16))) uint8_t lds2[PP ? STAGE : 16];
+    __shared__ __attribute__((aligned(PP ? 1024 : 16))) uint8_t lds3[PP ? STAGE : 16];
     constexpr int NB = STAGE / 1024;           // 1 KiB blocks of a stage
     constexpr int NI = (NB + NW - 1) / NW;     // direct-to-LDS loads per wave per stage (block i NW + wave < NB)
     static_assert(NB * 1024 == STAGE, "stages of whole 1 KiB blocks");
@@ -715,7 +719,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     int tt[TN];
     uint32_t cg[TN], sg[TN], zg[TN];
     // the per-lane offsets of an item
-    auto set_item = [&](int item) {
+    auto set_item = [&](int item) __attribute__((always_inline)) {
         tok0 = (item / nwt) * BM;
         tile0 = (item % nwt) * WTILES + wn * TN * 2;
         // activations: load i of this wave fills LDS block i NW + wave, whose lane l writes row 8 block + l / 8, slot
@@ -739,7 +743,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         u32x4 c[TN][2][CW];  // per output block: the two pieces (x CW words for int8)
         float s[TN], off[TN];
     };
-    auto wload = [&](int g, WFrag& f) {
+    auto wload = [&](int g, WFrag& f) __attribute__((always_inline)) {
         const uint8_t* cb = (const uint8_t*)a.codes + (size_t)g * 64 * CW * 16;
         const size_t sq = ((size_t)(g >> 2) * tiles * TILE * 4 + (g & 3)) * ((F & F_S32) ? 4 : 2);
 #pragma unroll
@@ -766,7 +770,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         }
     };
     // B fragment of output block t for k16 step kk (0..7) of the group
-    auto dequant = [&](const WFrag& f, int t, int kk) -> bf16x8 {
+    auto dequant = [&](const WFrag& f, int t, int kk) __attribute__((always_inline)) -> bf16x8 {
         const int pc = kk & 1, i = kk >> 1;
         if (F & F_BF16) return __builtin_bit_cast(bf16x8, f.c[t][pc][i]);  // step kk's piece as stored
         if (F & F_I8)  // int8: word pair (2e, 2e + 1) of half h, for k32 step i = 2h + e
@@ -775,7 +779,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     };
 
     f32x16 acc[BMB][TN];
-    auto clear = [&]() {
+    auto clear = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
@@ -786,7 +790,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
 
     // one stage (64 columns, half hh of the group) from LDS buffer `buf`: the A fragments of k16 step s16 + 1 are read
     // while step s16's MFMAs run
-    auto compute = [&](int buf, int hh, const WFrag& w) {
+    auto compute = [&](int buf, int hh, const WFrag& w) __attribute__((always_inline)) {
         const uint8_t* lb = buf ? lds1 : lds0;
         // raised issue priority while this wave's MFMAs run: of the SIMD's waves, the one in its MFMA phase issues
         // first and the other fills the gaps with its loads, LDS stores and barrier (measured: equal or faster on
@@ -818,7 +822,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // into lds1 and the next group's weights into registers, then stage 2g + 1 from lds1 while stage 2g + 2 loads into
     // lds0; each stage ends with a wait for its activation loads (the weight loads issued after them may stay in
     // flight) and one barrier.
-    auto stage_issue = [&](int st, uint8_t* buf) {
+    auto stage_issue = [&](int st, uint8_t* buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
             if (NB % NW == 0 || i * NW + wave < NB)  // wave-uniform
@@ -827,7 +831,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     };
     // weight loads a wload issues (code pieces, scale, zero point): what may stay in flight after a stage's x loads
     constexpr int WLOADS = TN * (2 * CW + ((F & (F_PERCH | F_BF16)) ? 0 : 1) + ((F & F_ZP) ? 1 : 0));
-    auto run = [&](int g0, int g1) {
+    auto run = [&](int g0, int g1) __attribute__((always_inline)) {
         clear();
         WFrag wcur, wnxt;
         stage_issue(2 * g0, lds0);
@@ -851,9 +855,91 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             wcur = wnxt;
         }
     };
+    // Ping-pong (PP: 256 x 256 items on 8 waves, no zero points, no fused LoRA). The SIMD's two waves (w and w + 4)
+    // take turns: while one runs a group's 64 MFMAs (raised issue priority, A fragments read six ahead through a
+    // register ring), the other dequantizes its weights for its next group into registers; a workgroup barrier ends
+    // each half. Activations: a group's two stages in one pair of LDS buffers while the next group's load into the
+    // other pair. Against the shared schedule above, same box, M = 2048: int4 (5120, 17408) / (17408, 5120) +2-3%,
+    // int8 +1-3.5% (MFMA busy 0.540 -> 0.564 and 0.564 -> 0.599, at a slightly lower clock); with zero points and with
+    // the fused LoRA delta it measured 5-8% slower, so those keep the shared schedule.
+    bf16x8 bwg[2 * PF_K16][TN];  // a group's B fragments, dequantized a half ahead of their MFMAs
+    auto deq_group = [&](const WFrag& w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kk = 0; kk < 2 * PF_K16; kk++)
+#pragma unroll
+            for (int t = 0; t < TN; t++) bwg[kk][t] = dequant(w, t, kk);
+    };
+    // the group's 16 k16 steps from the two stage buffers
+    auto mfma_group = [&](const uint8_t* la, const uint8_t* lb2) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_setprio(1);
+        constexpr int NF = 2 * PF_K16 * BMB, LA = 6;  // A fragments (k16 step f / BMB, token block f % BMB); ring
+        auto addr = [&](int f) __attribute__((always_inline)) -> const u32x4* {
+            const int kk = f / BMB, bb = f % BMB;
+            return (const u32x4*)((kk < PF_K16 ? la : lb2) + xr[kk % PF_K16] + bb * 32 * PF_ROW);
+        };
+        u32x4 ring[LA];
+#pragma unroll
+        for (int f = 0; f < LA; f++) ring[f] = *addr(f);
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const u32x4 cur = ring[f % LA];
+            if (f + LA < NF) ring[f % LA] = *addr(f + LA);
+#pragma unroll
+            for (int t = 0; t < TN; t++) acc[f % BMB][t] = mfma32(cur, bwg[f / BMB][t], acc[f % BMB][t]);
+        }
+        // the order above, kept by the scheduler: LA reads, then each MFMA followed by the next read
+        __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
+#pragma unroll
+        for (int f = 0; f < NF - LA; f++) {
+            __builtin_amdgcn_sched_group_barrier(0x8, TN, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x8, TN * LA, 0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // group g of a run for ping-pong role GRP (0: MFMAs first): its stages in buffers (a0, a1), the next group's
+    // loading into (b0, b1), whose last readers passed the previous barrier
+    auto pp_group = [&](auto GRP, int g, int g1, uint8_t* a0, uint8_t* a1, uint8_t* b0, uint8_t* b1, WFrag& wcur,
+                        WFrag& wnxt) __attribute__((always_inline)) {
+        constexpr int grp = decltype(GRP)::value;
+        const bool more = g + 1 < g1;
+        if (more) {
+            stage_issue(2 * g + 2, b0);
+            stage_issue(2 * g + 3, b1);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the activation loads
+        wload(more ? g + 1 : g, wnxt);
+        if (grp == 0) mfma_group(a0, a1);
+        else deq_group(wcur);
+        __syncthreads();
+        if (grp == 0) {
+            if (more) deq_group(wnxt);
+        } else {
+            mfma_group(a0, a1);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // the next group's activations (and weights) landed
+        __syncthreads();
+        wcur = wnxt;
+    };
+    // acc = the current item's product over groups [g0, g1), ping-pong role GRP
+    auto run_pp = [&](auto GRP, int g0, int g1) __attribute__((always_inline)) {
+        constexpr int grp = decltype(GRP)::value;
+        clear();
+        WFrag wcur, wnxt;
+        stage_issue(2 * g0, lds0);
+        stage_issue(2 * g0 + 1, lds1);
+        wload(g0, wcur);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (grp == 0) deq_group(wcur);
+        for (int g = g0; g < g1; g += 2) {  // two groups per pass: the buffer pairs stay known at compile time
+            pp_group(GRP, g, g1, lds0, lds1, lds2, lds3, wcur, wnxt);
+            if (g + 1 < g1) pp_group(GRP, g + 1, g1, lds2, lds3, lds0, lds1, wcur, wnxt);
+        }
+    };
     // epilogue of the current item: acc[bb][t][v] = D[token tok0 + wtok0 + 32 bb + 8 (v / 4) + 4 lh + v % 4]
     // [output 32-block t, l32]
-    auto epilogue = [&]() {
+    auto epilogue = [&]() __attribute__((always_inline)) {
         if (F & F_PERCH) {  // the row's scale after the exact integer sum
 #pragma unroll
             for (int t = 0; t < TN; t++) {
@@ -942,14 +1028,18 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     constexpr int NQ = NACC / 4, SK_QC = NQ >= 32 ? 16 : NQ / 2;
     const __amdgpu_buffer_rsrc_t skr = __builtin_amdgcn_make_buffer_rsrc(a.sk_part, 0, (int)PF_SK_PART_BYTES,
                                                                          BUF_RSRC_WORD3);
-    auto sk_off = [&](int slot, int w, int l) -> uint32_t {
+    auto sk_off = [&](int slot, int w, int l) __attribute__((always_inline)) -> uint32_t {
         return (uint32_t)((((size_t)slot * NW + w) * NQ * 64 + l) * 16);
     };
     const int first_item = u / G;
+    // the work loop, instantiated once per ping-pong role (a role known at compile time keeps the compiler from
+    // merging the two roles' live registers, which spilled)
+    auto work = [&](auto GRP) __attribute__((always_inline)) {
     while (u < u1) {
         const int it = u / G, g0 = u - it * G, g1 = min(G, g0 + (u1 - u));
         set_item(it);
-        run(g0, g1);
+        if constexpr (PP) run_pp(GRP, g0, g1);
+        else run(g0, g1);
         u += g1 - g0;
         if (a.ks == 1 && (g0 != 0 || g1 != G)) {
             // a cut item (stream-K): write this segment's partial to slot 2 s (+1 unless it is this workgroup's
@@ -1003,6 +1093,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         }
         epilogue();
     }
+    };
+    if (PP && (wave >> 2) != 0) work(std::integral_constant<int, 1>{});
+    else work(std::integral_constant<int, 0>{});
     if (EPI == EPI_ARGMAX) argmax_finish(a, threadIdx.x, blockDim.x);
 }
 
