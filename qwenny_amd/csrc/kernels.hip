@@ -687,7 +687,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
     // the ping-pong schedule (below) keeps a whole group's two stages and the next group's in flight: two more
-    constexpr bool PP = NW == 8 && WM == 1 && TN == 1 && !(F & F_ZP) && !LORA;
+    constexpr bool PP = NW == 8 && WM == 1 && TN == 1;
     __shared__ __attribute__((aligned(PP ? 1024 : 16))) uint8_t lds2[PP ? STAGE : 16];
     __shared__ __attribute__((aligned(PP ? 1024 : 16))) uint8_t lds3[PP ? STAGE : 16];
     constexpr int NB = STAGE / 1024;           // 1 KiB blocks of a stage
@@ -739,43 +739,53 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             zg[t] = (uint32_t)(zero_idx(tt[t], tiles, 0, l16) * 2);
         }
     };
+    // a group's weights as loaded: codes, and the raw scale and zero-point words, converted only where the group is
+    // dequantized (converted at the load, the compiler would hold the wave there for every load in flight)
     struct WFrag {
         u32x4 c[TN][2][CW];  // per output block: the two pieces (x CW words for int8)
-        float s[TN], off[TN];
+        uint32_t sr[TN], zr[TN];
+        int zs;  // the group's zero point: bits zs .. zs + 3 of zr
     };
     auto wload = [&](int g, WFrag& f) __attribute__((always_inline)) {
         const uint8_t* cb = (const uint8_t*)a.codes + (size_t)g * 64 * CW * 16;
         const size_t sq = ((size_t)(g >> 2) * tiles * TILE * 4 + (g & 3)) * ((F & F_S32) ? 4 : 2);
+        f.zs = 4 * (g & 3);
 #pragma unroll
         for (int t = 0; t < TN; t++) {
 #pragma unroll
             for (int pc = 0; pc < 2; pc++)
 #pragma unroll
                 for (int h = 0; h < CW; h++) f.c[t][pc][h] = *(const u32x4*)(cb + cg[t] + (h * 64 + 32 * pc) * 16);
-            if (F & F_BF16) {
-                f.s[t] = 1.0f;  // the weights themselves
-                f.off[t] = 0.0f;
-            } else if (F & F_PERCH) {
-                f.s[t] = 1.0f;  // exact integers q = stored - 128; the row scale comes after the sum
-                f.off[t] = -128.0f;
-            } else {
+            f.sr[t] = f.zr[t] = 0;
+            if (!(F & (F_BF16 | F_PERCH))) {
                 const uint8_t* sp = (const uint8_t*)a.scales + sq + sg[t];
-                f.s[t] = (F & F_S32) ? *(const float*)sp : bf16_bits_f(*(const uint16_t*)sp);
-                int z = (F & F_I8) ? 128 : 8;
+                f.sr[t] = (F & F_S32) ? *(const uint32_t*)sp : (uint32_t)*(const uint16_t*)sp;
                 if (F & F_ZP)
-                    z = (*(const uint16_t*)((const uint8_t*)a.zeros + (size_t)(g >> 2) * tiles * TILE * 2 + zg[t]) >>
-                         (4 * (g & 3))) & 15;
-                f.off[t] = -(float)z * f.s[t];
+                    f.zr[t] = *(const uint16_t*)((const uint8_t*)a.zeros + (size_t)(g >> 2) * tiles * TILE * 2 + zg[t]);
             }
         }
     };
+    // the scale s and offset -z s of output block t
+    auto scale_off = [&](const WFrag& f, int t, float& sc, float& off) __attribute__((always_inline)) {
+        if (F & F_BF16) {
+            sc = 1.0f;  // the weights themselves
+            off = 0.0f;
+        } else if (F & F_PERCH) {
+            sc = 1.0f;  // exact integers q = stored - 128; the row scale comes after the sum
+            off = -128.0f;
+        } else {
+            sc = __uint_as_float((F & F_S32) ? f.sr[t] : f.sr[t] << 16);
+            const int z = (F & F_ZP) ? (int)((f.zr[t] >> f.zs) & 15u) : ((F & F_I8) ? 128 : 8);
+            off = -(float)z * sc;
+        }
+    };
     // B fragment of output block t for k16 step kk (0..7) of the group
-    auto dequant = [&](const WFrag& f, int t, int kk) __attribute__((always_inline)) -> bf16x8 {
+    auto dequant = [&](const WFrag& f, int t, int kk, float sc, float off) __attribute__((always_inline)) -> bf16x8 {
         const int pc = kk & 1, i = kk >> 1;
         if (F & F_BF16) return __builtin_bit_cast(bf16x8, f.c[t][pc][i]);  // step kk's piece as stored
         if (F & F_I8)  // int8: word pair (2e, 2e + 1) of half h, for k32 step i = 2h + e
-            return i8_scaled(f.c[t][pc][i >> 1][2 * (i & 1)], f.c[t][pc][i >> 1][2 * (i & 1) + 1], f.s[t], f.off[t]);
-        return i4_scaled(f.c[t][pc][0][i], f.s[t], f.off[t]);
+            return i8_scaled(f.c[t][pc][i >> 1][2 * (i & 1)], f.c[t][pc][i >> 1][2 * (i & 1) + 1], sc, off);
+        return i4_scaled(f.c[t][pc][0][i], sc, off);
     };
 
     f32x16 acc[BMB][TN];
@@ -792,6 +802,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // while step s16's MFMAs run
     auto compute = [&](int buf, int hh, const WFrag& w) __attribute__((always_inline)) {
         const uint8_t* lb = buf ? lds1 : lds0;
+        float wsc[TN], woff[TN];
+#pragma unroll
+        for (int t = 0; t < TN; t++) scale_off(w, t, wsc[t], woff[t]);
         // raised issue priority while this wave's MFMAs run: of the SIMD's waves, the one in its MFMA phase issues
         // first and the other fills the gaps with its loads, LDS stores and barrier (measured: equal or faster on
         // every prefill shape, +9% on (17408, 5120) at 512 tokens)
@@ -808,7 +821,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             }
             bf16x8 bw[TN];
 #pragma unroll
-            for (int t = 0; t < TN; t++) bw[t] = dequant(w, t, PF_K16 * hh + s16);
+            for (int t = 0; t < TN; t++) bw[t] = dequant(w, t, PF_K16 * hh + s16, wsc[t], woff[t]);
 #pragma unroll
             for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
@@ -855,19 +868,22 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             wcur = wnxt;
         }
     };
-    // Ping-pong (PP: 256 x 256 items on 8 waves, no zero points, no fused LoRA). The SIMD's two waves (w and w + 4)
+    // Ping-pong (PP: 256 x 256 items on 8 waves). The SIMD's two waves (w and w + 4)
     // take turns: while one runs a group's 64 MFMAs (raised issue priority, A fragments read six ahead through a
     // register ring), the other dequantizes its weights for its next group into registers; a workgroup barrier ends
     // each half. Activations: a group's two stages in one pair of LDS buffers while the next group's load into the
     // other pair. Against the shared schedule above, same box, M = 2048: int4 (5120, 17408) / (17408, 5120) +2-3%,
-    // int8 +1-3.5% (MFMA busy 0.540 -> 0.564 and 0.564 -> 0.599, at a slightly lower clock); with zero points and with
-    // the fused LoRA delta it measured 5-8% slower, so those keep the shared schedule.
+    // int8 +1-3.5%, zero points +3-5%, the fused LoRA delta 0 to +5% (MFMA busy 0.540 -> 0.564 and 0.564 -> 0.599, at a
+    // slightly lower clock).
     bf16x8 bwg[2 * PF_K16][TN];  // a group's B fragments, dequantized a half ahead of their MFMAs
     auto deq_group = [&](const WFrag& w) __attribute__((always_inline)) {
+        float wsc[TN], woff[TN];
+#pragma unroll
+        for (int t = 0; t < TN; t++) scale_off(w, t, wsc[t], woff[t]);
 #pragma unroll
         for (int kk = 0; kk < 2 * PF_K16; kk++)
 #pragma unroll
-            for (int t = 0; t < TN; t++) bwg[kk][t] = dequant(w, t, kk);
+            for (int t = 0; t < TN; t++) bwg[kk][t] = dequant(w, t, kk, wsc[t], woff[t]);
     };
     // the group's 16 k16 steps from the two stage buffers
     auto mfma_group = [&](const uint8_t* la, const uint8_t* lb2) __attribute__((always_inline)) {
