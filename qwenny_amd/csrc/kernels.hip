@@ -363,32 +363,36 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) 
 #pragma unroll
             for (int r = 0; r < NR; r++) acc[b][t][r] = 0.0f;
 
+    // the activation pieces this thread stages (the same in every super-chunk): the first XPT of its pieces are loaded
+    // ahead of the weights; their rows (the argmax's gathered rows) are looked up once, here, not in every super-chunk
+    const int rowc = CH * 16;  // 16-byte pieces per staged row
+    const int npieces = M * rowc;
+    constexpr int XPT = PRIV ? 0 : TB;
+    int xo[XPT > 0 ? XPT : 1];            // LDS offset (-1: none)
+    const __bf16* xsrc[XPT > 0 ? XPT : 1];  // source, before the super-chunk's column offset
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int p = tid + i * nthr;
+        const int tok = min(p / rowc, M - 1), pc = p - (p / rowc) * rowc;
+        xo[i] = p < npieces ? tok * xpitch + 8 * pc : -1;
+        xsrc[i] = (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * (p < npieces ? pc : 0);
+    }
+    const __bf16* xwsrc = (const __bf16*)a.x + (size_t)(PRIV && a.xrows ? a.xrows[0] : 0) * a.ldx + 8 * lane;
+
     for (int c = c0; c < c1; c++) {
         const int gs = c * CH;              // first group of the super-chunk
         const int gw = gs + wk * NG;        // this wave's first group
         // 1. the super-chunk's activations (M rows of CH * 128 columns): the first XPT pieces per thread are loaded
         //    before the weights (loads complete in order, so staging them afterwards would wait for every weight),
         //    the rest, if any, afterwards
-        const int rowc = CH * 16;  // 16-byte pieces per row
-        const int npieces = M * rowc;
-        constexpr int XPT = PRIV ? 0 : TB;  // activation pieces each thread loads ahead of the weights
         u32x4 xv[XPT > 0 ? XPT : 1];
-        int xo[XPT > 0 ? XPT : 1];
         if constexpr (PRIV) {  // the wave's own 4 groups (64 pieces of 16 bytes), global -> LDS directly
-            __builtin_amdgcn_global_load_lds(
-                (const void*)((const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[0] : 0) * a.ldx + (size_t)gw * QG +
-                              8 * lane),
-                (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(xwsrc + (size_t)gw * QG),
+                                             (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int p = tid + i * nthr;
-            const int tok = min(p / rowc, M - 1), pc = p - (p / rowc) * rowc;
-            xo[i] = p < npieces ? tok * xpitch + 8 * pc : -1;
-            xv[i] = *(const u32x4*)((const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx +
-                                    (size_t)gs * QG + 8 * (p < npieces ? pc : 0));
-        }
+        for (int i = 0; i < XPT; i++) xv[i] = *(const u32x4*)(xsrc[i] + (size_t)gs * QG);
         // 2. this wave's weights: scales (4 groups per load), zero points, then codes group by group, all streamed
         //    (non-temporal: read once; measured 1-2% faster for the scales, 10% for the codes, than cached loads)
         uint32_t sraw[T][NG == 4 ? ((F & F_S32) ? 4 : 2) : 1];
