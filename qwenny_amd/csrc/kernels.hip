@@ -11,14 +11,16 @@
 // the MFMA sums x (128 + q) exactly in f32 per 128-column group, and the group's scale and zero point are applied
 // after it: acc += s (D - (128 + z) sum_k x), where sum_k x comes from one more MFMA against ones per k32 step (shared
 // by the wave's tiles). K is split over the waves of a workgroup (reduced through LDS) and, for plain products, over
-// the grid (the split-K partials of the output contract).
+// the grid (the split-K partials of the output contract). The activations are staged in LDS once per workgroup, or,
+// for one token of int4 without zero points, by each wave for itself (no workgroup barrier).
 //
 // prefill_kernel (m > 48): MFMA-bound. A workgroup computes up to 256 tokens x 256 outputs (8 waves of 256 x 32, or
 // 256 x 192 on 12 waves of 128 x 32, or smaller tiles for short steps); the activation tile goes global -> LDS directly
 // (global_load_lds) into double-buffered, XOR-swizzled 64-column stages, each wave dequantizes its own outputs'
 // weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), the workgroups are mapped
 // XCD-aware (an XCD's workgroups share a token tile's activations in its L2), and a badly filled last round is spread
-// over the resident workgroups by groups of K (stream-K).
+// over the resident workgroups by groups of K (stream-K). On 256 x 256 items the two waves of each SIMD ping-pong: one
+// runs a group's MFMAs while the other dequantizes its next group's weights.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
