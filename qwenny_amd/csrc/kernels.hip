@@ -839,8 +839,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // acc = the current item's product over groups [g0, g1). The activations go global -> LDS directly
     // (global_load_lds_dwordx4): stage 2g (the group's first 64 columns) is computed from lds0 while stage 2g + 1 loads
     // into lds1 and the next group's weights into registers, then stage 2g + 1 from lds1 while stage 2g + 2 loads into
-    // lds0; each stage ends with a wait for its activation loads (the weight loads issued after them may stay in
-    // flight) and one barrier.
+    // lds0; each stage ends with one workgroup barrier, whose fence also waits for this wave's loads in flight (the next
+    // stage's activations and the next group's weights: a barrier without the fence, leaving the weights in flight,
+    // measured the same here and slower in the ping-pong schedule).
     auto stage_issue = [&](int st, uint8_t* buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
@@ -848,8 +849,6 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             __builtin_amdgcn_global_load_lds((const void*)(xbase + (size_t)st * PF_ROW + xd[i]),
                                              (lds_ptr)(buf + (i * NW + wave) * 1024), 16, 0, 0);
     };
-    // weight loads a wload issues (code pieces, scale, zero point): what may stay in flight after a stage's x loads
-    constexpr int WLOADS = TN * (2 * CW + ((F & (F_PERCH | F_BF16)) ? 0 : 1) + ((F & F_ZP) ? 1 : 0));
     auto run = [&](int g0, int g1) __attribute__((always_inline)) {
         clear();
         WFrag wcur, wnxt;
@@ -861,11 +860,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             const bool more = g + 1 < g1;
             // stage 2g from lds0 while stage 2g + 1 loads into lds1 (the next group's weights behind it)
             stage_issue(2 * g + 1, lds1);
-            __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the x loads (the wait below counts on it)
+            __builtin_amdgcn_sched_barrier(0);  // the weight loads behind the activation loads
             wload(more ? g + 1 : g, wnxt);
             compute(0, 0, wcur);
-            // x loads done, the weight loads issued after them may stay in flight
-            __builtin_amdgcn_s_waitcnt((WLOADS & 15) | ((WLOADS >> 4) << 14) | (7 << 4) | (15 << 8));
             __syncthreads();
             if (more) stage_issue(2 * g + 2, lds0);
             compute(1, 1, wcur);
