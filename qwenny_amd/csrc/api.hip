@@ -426,6 +426,8 @@ int qh::gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void
         l.lora_tab = lora->tab;
         l.lora_tok_slot = lora->tok_slot;
         l.lora_slot_scale = lora->slot_scale;
+        l.lora_stage = lora->split == 1 && (lora->m_cols == 4 || lora->m_cols == 8 || lora->m_cols == 16 ||
+                                            lora->m_cols == 32) && ((uintptr_t)lora->xa & 15) == 0;
     }
     hipError_t e = launch(l);
     if (e != hipSuccess) return fail(QH_EHIP, "gemm launch: %s", hipGetErrorString(e));

@@ -55,6 +55,7 @@ struct Launch {
     // SwiGLU products to gate and up before the activation (kernels.hip lora_delta16 / lora_delta32)
     const float* lora_xa;        // the stacked A product's partials [lora_split][m][lora_cols]
     int lora_split, lora_cols, lora_rank;
+    int lora_stage;              // prefill: the item's xa rows staged in LDS (one split, 4 to 32 columns, aligned)
     const uint16_t* lora_b;      // B f16 [rows][lora_rank], the product's row order
     const int* lora_tab;         // module end rows (3 used), then each module's first column of xa (-1: none)
     const int* lora_tok_slot;

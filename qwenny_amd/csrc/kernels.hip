@@ -253,10 +253,12 @@ __device__ void lora_delta16(const Launch& a, int tile, int tok0, f32x4& d) {
 // The prefill kernel's layout (v_mfma_f32_32x32x2_f32): the deltas of a wave's TN blocks of 32 output rows (block t:
 // rows (tile0 + 2 t) 16 ..) for its BMB blocks of 32 tokens (block bb: tokens tok0 + 32 bb ..), accumulated into
 // acc[bb][t]; lane l holds D[token 8 (v / 4) + 4 (l / 32) + v % 4][row l % 32], v = 0..15. Loads are batched for
-// latency: the tokens' slot scales for every block at once, each output block's B run once, the xa runs of NBB token
-// blocks at a time.
+// latency: the tokens' slot scales for every block at once, each lane's B run once, and xa either from the item's rows
+// staged in LDS (xs: one split, 4-32 columns; row r's 16-byte chunk k at slot k ^ (r mod chunks per row), rows from
+// xs_row0) or, otherwise, the xa runs of NBB token blocks at a time from global memory.
 template <bool SILU, int BMB, int TN>
-__device__ void lora_item32(const Launch& a, int tile0, int tok0, f32x16 (&acc)[BMB][TN]) {
+__device__ void lora_item32(const Launch& a, int tile0, int tok0, f32x16 (&acc)[BMB][TN], const uint8_t* xs = nullptr,
+                            int xs_row0 = 0) {
     // one code path for every rank (a switch over ranks multiplies the epilogue's code and spills registers): the
     // H = R / 2 contraction steps run C at a time, lane group h taking k = h H + i
     constexpr int C = 4;                     // steps whose operands are in registers at a time (H is a multiple)
@@ -277,18 +279,58 @@ __device__ void lora_item32(const Launch& a, int tile0, int tok0, f32x16 (&acc)[
         if (o0 >= a.rows) break;  // wave-uniform
         const int o = min(o0 + l32, a.rows - 1), mod = lora_module_of<SILU>(a, o);
         const int mlo = lora_module_of<SILU>(a, o0), mhi = lora_module_of<SILU>(a, min(o0 + 31, a.rows - 1));
+        // this lane's B run (row o, columns h H .. h H + H), loaded once for every module and step as f16 pairs (H is 4 to
+        // 32): one load instead of a dependent one per module and step
+        uint32_t bw[16];
+        {
+            const _Float16* bp = (const _Float16*)a.lora_b + (size_t)o * a.lora_rank + h * H;
+            if (H == 4) {  // rank 8: the run is 8 bytes (a 16-byte load would pass the last row's end)
+                const unsigned long long v = *(const unsigned long long*)bp;
+                bw[0] = (uint32_t)v, bw[1] = (uint32_t)(v >> 32);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (8 * q < H) {
+                        const u32x4 v = ((const u32x4*)bp)[q];
+                        bw[4 * q] = v.x, bw[4 * q + 1] = v.y, bw[4 * q + 2] = v.z, bw[4 * q + 3] = v.w;
+                    }
+            }
+        }
         for (int m = mlo; m <= mhi; m++) {
             const int c0 = lora_off(a, m);
             if (c0 < 0) continue;  // wave-uniform
             for (int i0 = 0; i0 < H; i0 += C) {
                 float bv[C];
-                lora_b_run<C>(a, o, h * H + i0, mod == m && o0 + l32 < a.rows, bv);
+                const bool keep = mod == m && o0 + l32 < a.rows;
+#pragma unroll
+                for (int i = 0; i < C; i += 2) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int q = 0; q < 16; q++)
+                        if (q == (i0 + i) >> 1) w = bw[q];
+                    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)w),
+                                   hi = __builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+                    bv[i] = keep ? (float)lo : 0.0f;
+                    bv[i + 1] = keep ? (float)hi : 0.0f;
+                }
                 // (loops over accumulators fully unrolled: an indexed register array would live in scratch memory)
 #pragma unroll
                 for (int b0 = 0; b0 < BMB; b0 += NBB) {
                     float xv[NBB][C];
+                    if (xs) {  // staged in LDS: row r's 16-byte chunk k at slot k ^ (r mod chunks per row)
+                        const int cpr = a.lora_cols >> 2, k = (c0 + h * H + i0) >> 2;
 #pragma unroll
-                    for (int j = 0; j < NBB; j++) lora_xs_run<C>(a, tok[b0 + j], c0 + h * H + i0, s[b0 + j], xv[j]);
+                        for (int j = 0; j < NBB; j++) {
+                            const int r = xs_row0 + 32 * (b0 + j) + l32;
+                            const f32x4 v = *(const f32x4*)(xs + (r * cpr + (k ^ (r & (cpr - 1)))) * 16);
+#pragma unroll
+                            for (int i = 0; i < C; i++) xv[j][i] = v[i] * s[b0 + j];
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < NBB; j++)
+                            lora_xs_run<C>(a, tok[b0 + j], c0 + h * H + i0, s[b0 + j], xv[j]);
+                    }
 #pragma unroll
                     for (int j = 0; j < NBB; j++)
 #pragma unroll
@@ -700,7 +742,12 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     constexpr int NI = (NB + NW - 1) / NW;     // direct-to-LDS loads per wave per stage (block i NW + wave < NB)
     static_assert(NB * 1024 == STAGE, "stages of whole 1 KiB blocks");
     uint32_t xd[NI];                       // per-lane global byte offsets of those loads (stage 0)
-    __shared__ int sk_last;
+    // LoRA: the item's xa rows ([BM][lora_cols] f32, 16-byte chunks XOR-swizzled by row), staged while the item runs
+    __shared__ __attribute__((aligned(16))) uint8_t xa_lds[LORA ? BM * 32 * 4 : 16];
+    // the stream-K counter's answer, in lds2: no load writes it in kernels without the ping-pong schedule, and in
+    // those with it the next run first writes it after its prologue's barrier, which every wave passes only after
+    // reading the answer
+    int* const sk_last_p = (int*)lds2;
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave % WM, wn = wave / WM;
@@ -849,6 +896,20 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             __builtin_amdgcn_global_load_lds((const void*)(xbase + (size_t)st * PF_ROW + xd[i]),
                                              (lds_ptr)(buf + (i * NW + wave) * 1024), 16, 0, 0);
     };
+    // LoRA: the item's xa rows (tokens tok0 .., clamped to m - 1) go global -> LDS while the item runs; the run's
+    // barriers make them the workgroup's before the epilogue reads them
+    auto xa_stage = [&]() __attribute__((always_inline)) {
+        if constexpr (LORA) {
+            if (a.lora_stage) {
+                const int cpr = a.lora_cols >> 2, nblk = BM * cpr / 64;  // 16-byte chunks per row; 1 KiB blocks
+                for (int blk = wave; blk < nblk; blk += NW) {
+                    const int e = blk * 64 + lane, row = e / cpr, k = (e - row * cpr) ^ (row & (cpr - 1));
+                    const float* src = a.lora_xa + (size_t)min(tok0 + row, M - 1) * a.lora_cols + 4 * k;
+                    __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr)(xa_lds + blk * 1024), 16, 0, 0);
+                }
+            }
+        }
+    };
     auto run = [&](int g0, int g1) __attribute__((always_inline)) {
         clear();
         WFrag wcur, wnxt;
@@ -856,6 +917,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         wload(g0, wcur);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        xa_stage();
         for (int g = g0; g < g1; g++) {
             const bool more = g + 1 < g1;
             // stage 2g from lds0 while stage 2g + 1 loads into lds1 (the next group's weights behind it)
@@ -950,6 +1012,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         wload(g0, wcur);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        xa_stage();
         if (grp == 0) deq_group(wcur);
         for (int g = g0; g < g1; g += 2) {  // two groups per pass: the buffer pairs stay known at compile time
             pp_group(GRP, g, g1, lds0, lds1, lds2, lds3, wcur, wnxt);
@@ -972,7 +1035,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         // the LoRA delta: on partial 0 of a plain product, before the activation of a SwiGLU one
         if constexpr (LORA) {
             if (EPI == EPI_SILU || kslice == 0) {
-                lora_item32<EPI == EPI_SILU, BMB, TN>(a, tile0, tok0 + wtok0, acc);
+                lora_item32<EPI == EPI_SILU, BMB, TN>(a, tile0, tok0 + wtok0, acc, a.lora_stage ? xa_lds : nullptr,
+                                                      wtok0);
             }
         }
         unsigned long long key[BMB][16];
@@ -1076,10 +1140,10 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             const int sit = it - dp, su = sit * G;  // the item among the stream-K ones, its first unit
             const int sa = sk_owner(su, a.sk_q, a.sk_r), sb = sk_owner(su + G - 1, a.sk_q, a.sk_r);
             if (threadIdx.x == 0)
-                sk_last = __hip_atomic_fetch_add(a.sk_count + sit, 1u, __ATOMIC_RELAXED,
+                *sk_last_p = __hip_atomic_fetch_add(a.sk_count + sit, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(sb - sa);
             __syncthreads();
-            if (!sk_last) continue;  // uniform over the workgroup
+            if (!*sk_last_p) continue;  // uniform over the workgroup
             // the last segment to arrive: the sum of all segments' partials in segment order from zero (so that it does
             // not depend on the order of arrival), 16 registers at a time. When it is the item's first segment (the
             // usual case: it reached the item at the end of its range), its own share, the sum's first term, stays in

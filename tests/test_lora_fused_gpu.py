@@ -78,20 +78,21 @@ def test_lora_plain_fused(gemm, m, rank, split, ends):
                                                             max(np.sqrt(np.mean(delta_want ** 2)), 1e-30)))
 
 
-@pytest.mark.parametrize("m", [1, 5, 40, 64, 300])
-@pytest.mark.parametrize("rank", [8, 32])
-def test_lora_silu_fused(gemm, m, rank):
+# split 1 with 16 or 32 columns of xa: prefill kernels stage the item's xa rows in LDS; (2048, 2048 + 2048, K 512):
+# 256 x 256 items, the ping-pong schedule with the staged rows
+@pytest.mark.parametrize("m,rank,split,half,k", [(m, r, s, 512, 1024) for m in (1, 5, 40, 64, 300) for r in (8, 32)
+                                                 for s in (1, 2)] + [(2048, 16, 1, 2048, 512), (2048, 8, 2, 2048, 512)])
+def test_lora_silu_fused(gemm, m, rank, split, half, k):
     import torch
 
-    print(f"fused lora silu m={m} rank={rank}", flush=True)
-    k, half = 1024, 512
+    print(f"fused lora silu m={m} rank={rank} split={split} rows={2 * half} k={k}", flush=True)
     gate, up = make_quant(1500 + m, "i4", half, k), make_quant(1501 + m, "i4", half, k)
     mat = Mat.stack(gemm, [gate, up], silu=True)
     rows = 2 * half
     rng = np.random.default_rng(1502 + m)
     m_cols = 2 * rank
     tab = [INT_MAX] * 4 + [0, rank, -1, -1]
-    dev, host = _adapter(rng, rows, rank, 2, m, m_cols, tab)
+    dev, host = _adapter(rng, rows, rank, split, m, m_cols, tab)
     x = activations(1503 + m, "x", m, k)
     mid = torch.full((m, half), float("nan"), dtype=torch.bfloat16, device="cuda")
     assert gemm.run_lora(None, m, mat, to_dev(x), mid, Epi.Silu, dev) == 1
@@ -102,7 +103,7 @@ def test_lora_silu_fused(gemm, m, rank):
         np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
     packed = full[:, order]  # the product in its packed (SwiGLU) row order
     xa, b, tab_h, tok_slot, slot_scale = host
-    want = oracle.lora_silu(packed, xa, 2, b, rank, tab_h, tok_slot, slot_scale, m)
+    want = oracle.lora_silu(packed, xa, split, b, rank, tab_h, tok_slot, slot_scale, m)
     assert bf16_out_err(got, want) <= 1e-3
 
 
