@@ -734,7 +734,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // two objects, so that the compiler can tell the direct-to-LDS loads into one from the reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
-    // the ping-pong schedule (below) keeps a whole group's two stages and the next group's in flight: two more
+    // the ping-pong schedule (below) keeps a whole group's two stages and the next group's in flight: two more stage
+    // buffers
     constexpr bool PP = NW == 8 && WM == 1 && TN == 1;
     __shared__ __attribute__((aligned(PP ? 1024 : 16))) uint8_t lds2[PP ? STAGE : 16];
     __shared__ __attribute__((aligned(PP ? 1024 : 16))) uint8_t lds3[PP ? STAGE : 16];
@@ -933,10 +934,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             wcur = wnxt;
         }
     };
-    // Ping-pong (PP: 256 x 256 items on 8 waves). The SIMD's two waves (w and w + 4)
-    // take turns: while one runs a group's 64 MFMAs (raised issue priority, A fragments read six ahead through a
-    // register ring), the other dequantizes its weights for its next group into registers; a workgroup barrier ends
-    // each half. Activations: a group's two stages in one pair of LDS buffers while the next group's load into the
+    // Ping-pong (PP: 256 x 256 items on 8 waves). The SIMD's two waves (w and w + 4) take turns: while one runs a
+    // group's 64 MFMAs (raised issue priority, A fragments read six ahead through a register ring), the other
+    // dequantizes its weights for its next group into registers; a workgroup barrier ends each half. Activations: a group's two stages in one pair of LDS buffers while the next group's load into the
     // other pair. Against the shared schedule above, same box, M = 2048: int4 (5120, 17408) / (17408, 5120) +2-3%,
     // int8 +1-3.5%, zero points +3-5%, the fused LoRA delta 0 to +5% (MFMA busy 0.540 -> 0.564 and 0.564 -> 0.599, at a
     // slightly lower clock).
