@@ -107,6 +107,40 @@ def test_lora_silu_fused(gemm, m, rank, split, half, k):
     assert bf16_out_err(got, want) <= 1e-3
 
 
+# Prefill products stage a one-split xa of 4-32 columns in LDS and read other forms from global memory: the same
+# adapter given as one partial or as two (the second all zeros) must give the same outputs bit for bit (the sums run
+# in the same order; 0 + p is p exactly). Plain (stream-K and whole items) and SwiGLU (the ping-pong 256 x 256 items).
+@pytest.mark.parametrize("epi,m,half,k", [("plain", 256, 2048, 2048), ("plain", 2048, 2048, 512),
+                                           ("silu", 2048, 2048, 512)])
+def test_lora_staged_xa_matches_global(gemm, epi, m, half, k):
+    import torch
+
+    print(f"staged xa {epi} m={m} rows={2 * half} k={k}", flush=True)
+    rank, rows = 16, 2 * half
+    gate, up = make_quant(1700, "i4", half, k), make_quant(1701, "i4", half, k)
+    mat = Mat.stack(gemm, [gate, up], silu=epi == "silu")
+    rng = np.random.default_rng(1702)
+    m_cols = 2 * rank
+    tab = [half, INT_MAX, INT_MAX, INT_MAX, 0, rank, -1, -1]
+    dev, host = _adapter(rng, rows, rank, 1, m, m_cols, tab)
+    xa2 = torch.cat([dev[0], torch.zeros_like(dev[0])])  # the same xa as two partials
+    dev2 = (xa2, 2) + dev[2:]
+    x = to_dev(activations(1703, "x", m, k))
+    outs = []
+    for lora in (dev, dev2):
+        if epi == "silu":
+            y = torch.full((m, half), float("nan"), dtype=torch.bfloat16, device="cuda")
+            assert gemm.run_lora(None, m, mat, x, y, Epi.Silu, lora) == 1
+        else:
+            sp = mat.split(m)
+            y = torch.full((sp * m * rows,), float("nan"), dtype=torch.float32, device="cuda")
+            assert gemm.run_lora(None, m, mat, x, y, Epi.Plain, lora) == sp
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    assert torch.equal(outs[0].view(torch.int16) if epi == "silu" else outs[0].view(torch.int32),
+                       outs[1].view(torch.int16) if epi == "silu" else outs[1].view(torch.int32))
+
+
 def test_lora_fused_rejects(gemm):
     import torch
 
