@@ -173,9 +173,19 @@ int qh_mat_describe(const qh_mat* m, qh_mat_desc* out);
 /* Copy a device matrix's packed buffers back to the host (sizes from qh_mat_describe); zeros may be NULL. */
 int qh_mat_download(const qh_mat* m, void* codes, void* scales, void* zeros);
 
-/* Split-K factor a plain product of n tokens uses on m (core.rs Mat::split): the skinny kernel's K chunks up to 48
- * tokens, 1-16 K slices (slices x tokens <= 2048) for 49-512, 1 above. No launch; the same value qh_gemm returns. */
+/* Split-K factor a plain product of n tokens uses on m (core.rs Mat::split): the skinny kernel's K chunks where it
+ * takes the product (qh_mat_kernel), 1-16 K slices (slices x tokens <= 2048) on the prefill kernel up to 512
+ * tokens, 1 above. No launch; the same value qh_gemm returns. */
 int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n);
+
+/* Which kernel a product of n tokens (qh_gemm's n, or n_out for QH_EPI_ARGMAX) with epilogue `epi` runs on m:
+ * QH_KERNEL_SKINNY (exact products of the dequantized weights) or QH_KERNEL_PREFILL (weights rounded to bf16 once;
+ * both within the bf16-operand bound). No counterpart in the reference, whose Marlin kernel serves every token count:
+ * for callers and tests that need to know which numerics a product has. The skinny kernel takes up to 48 tokens,
+ * except plain split-K products of symmetric int4 matrices of at least 2^26 weights from 33 tokens. No launch. */
+#define QH_KERNEL_SKINNY 1
+#define QH_KERNEL_PREFILL 2
+int qh_mat_kernel(const qh_ctx* ctx, const qh_mat* m, size_t n, int epi, int whole);
 
 /* part_len (core.rs:315-318): floats the plain products of `mats` write at most, for up to `max_tok` tokens. */
 size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok);

@@ -61,6 +61,7 @@ SIGNATURES = {
     "qh_mat_describe": (I, [P, ctypes.POINTER(MatDesc)]),
     "qh_mat_download": (I, [P, P, P, P]),
     "qh_mat_split": (I, [P, P, S]),
+    "qh_mat_kernel": (I, [P, P, S, I, I]),
     "qh_part_len": (S, [P, P, S, S]),
     "qh_gemm": (I, [P, P, P, P, S, S, P, S, P, I, P, I]),
     "qh_gemm_noalloc": (I, [P, P, P, P, S, S, P, S, P, I, P, I]),

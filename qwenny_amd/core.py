@@ -250,6 +250,14 @@ class Mat:
         """Split-K factor of a plain product of n tokens (src/cuda/core.rs Mat::split)."""
         return check(lib().qh_mat_split(self._gemm._ctx, self._m, n))
 
+    def kernel(self, n, epi=None, whole=False):
+        """"skinny" or "prefill": the kernel a product of n tokens (n_out logit rows for the argmax) with epilogue
+        `epi` (Plain by default) runs on this matrix. The skinny kernel's products are exact products of the
+        dequantized weights; the prefill kernel rounds each weight to bf16 once."""
+        e = Epi.Plain if epi is None else epi
+        k = check(lib().qh_mat_kernel(self._gemm._ctx, self._m, n, int(e), int(bool(whole))))
+        return "skinny" if k == 1 else "prefill"
+
     def download(self):
         """The packed buffers (codes, scales, zeros) back on the host."""
         d = self.desc()

@@ -30,6 +30,7 @@ struct qh_ctx {
     void* sk_scratch;
     int stream_k;
     int skinny_plain_wk;    // skinny kernel, plain products: wave rows over K per workgroup (1; QH_SKINNY_PLAIN_WK)
+    int pf_from;            // plain products from this many tokens take the prefill kernel (QH_PF_FROM, tuning)
 };
 
 int qh::ctx_device(const qh_ctx* ctx) { return ctx->device; }
@@ -95,7 +96,8 @@ extern "C" int qh_open(int device, qh_ctx** out) {
                       std::min(64, std::max(1, env_int("QH_SKINNY_FILL", 8))),
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
                       std::min(9, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1)),
-                      std::min(4, std::max(1, env_int("QH_SKINNY_PLAIN_WK", 1)))};
+                      std::min(4, std::max(1, env_int("QH_SKINNY_PLAIN_WK", 1))),
+                      std::max(1, env_int("QH_PF_FROM", SKINNY_MAX_M + 1))};
     return QH_OK;
 }
 
@@ -313,6 +315,20 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
     return Partition{wt, wt * wk, 1, ng};
 }
 
+// Whether the skinny kernel takes a product of m tokens (else the prefill kernel): up to SKINNY_MAX_M tokens, except
+// plain split-K products of symmetric int4 matrices of at least PF_FROM33_WEIGHTS weights from 33 tokens (three
+// 16-token blocks per skinny wave), where the prefill kernel's K slices are faster (measured on the 27B shapes
+// (5120, 17408) and (17408, 5120) at 33-48 tokens: 21-23 against 26-28 us per product, 25-27 against 33-39 us with
+// the partials summed; on the 4B and smaller 27B shapes, 31M weights and below, the skinny kernel stays ahead).
+// QH_PF_FROM (tuning) moves every plain product from that many tokens to the prefill kernel instead.
+static bool use_skinny(const qh_ctx* ctx, const qh_mat* w, size_t m, int epi, int whole) {
+    if (m > (size_t)SKINNY_MAX_M) return false;
+    if (epi != QH_EPI_PLAIN) return true;
+    if (ctx->pf_from <= SKINNY_MAX_M) return m < (size_t)ctx->pf_from;
+    const bool i4 = w->wt == QH_WT_I4 || w->wt == QH_WT_I4_S32;
+    return !(m > 32 && !whole && i4 && w->rows * w->cols >= PF_FROM33_WEIGHTS);
+}
+
 // The launch of a product of m tokens (epi, x, y and keys as qh_gemm takes them; `whole`: one partial).
 static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, size_t ldx, size_t m,
                           const int32_t* out_rows, void* y, int epi, uint64_t* keys, int whole, void* stream,
@@ -347,7 +363,8 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
     l.nib_mask = 0x000F000Fu;
     l.ks = 1;
     l.whole = whole;
-    if (m <= (size_t)SKINNY_MAX_M) {
+    l.skinny = use_skinny(ctx, w, m, epi, whole);
+    if (l.skinny) {
         Partition p = skinny_partition(ctx, w, m, epi == QH_EPI_PLAIN && !whole);
         l.tile_waves = p.tile_waves;
         l.waves = p.waves;
@@ -367,13 +384,19 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
 extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
     if (!ctx || !m) return fail(QH_EINVAL, "split: null");
     if (n == 0) return 1;
-    if (n <= (size_t)SKINNY_MAX_M) return skinny_partition(ctx, m, n, true).split;
+    if (use_skinny(ctx, m, n, QH_EPI_PLAIN, 0)) return skinny_partition(ctx, m, n, true).split;
     if (n > (size_t)PF_KS_MAX_M || n > (1u << 24)) return 1;
     Launch l = make_launch(ctx, m, nullptr, m->cols, n, nullptr, nullptr, QH_EPI_PLAIN, nullptr, 0, nullptr,
                            Scratch{ctx->argmax_scratch, ctx->sk_scratch});
     l.dry_run = 1;
     if (hipError_t e = launch(l); e != hipSuccess) return fail(QH_EHIP, "split: %s", hipGetErrorString(e));
     return l.split;
+}
+
+extern "C" int qh_mat_kernel(const qh_ctx* ctx, const qh_mat* m, size_t n, int epi, int whole) {
+    if (!ctx || !m) return fail(QH_EINVAL, "kernel: null");
+    if (epi != QH_EPI_PLAIN && epi != QH_EPI_SILU && epi != QH_EPI_ARGMAX) return fail(QH_EINVAL, "epilogue %d", epi);
+    return use_skinny(ctx, m, n, epi, whole) ? QH_KERNEL_SKINNY : QH_KERNEL_PREFILL;
 }
 
 extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, size_t max_tok) {
@@ -407,7 +430,7 @@ int qh::gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void
     if (m > (1u << 24) || w->rows > (1u << 30) || ldx > (1u << 30)) return fail(QH_EINVAL, "gemm: sizes too large");
     // the prefill kernel addresses activation rows (the n token rows, also those the argmax gathers) with 32-bit byte
     // offsets from x
-    if (m > (size_t)SKINNY_MAX_M && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
+    if (!use_skinny(ctx, w, m, epi, whole) && ((std::max(n, m) - 1) * ldx + w->cols) * 2 > 0xffffffffu)
         return fail(QH_EINVAL, "gemm: %zu token rows of %zu elements: x must fit in 4 GiB", n, ldx);
     Launch l = make_launch(ctx, w, x, ldx, m, out_rows, y, epi, keys, whole, stream, sc);
     if (lora) {

@@ -55,6 +55,7 @@ struct Launch {
     // SwiGLU products to gate and up before the activation (kernels.hip lora_delta16 / lora_delta32)
     const float* lora_xa;        // the stacked A product's partials [lora_split][m][lora_cols]
     int lora_split, lora_cols, lora_rank;
+    int skinny;                  // the skinny kernel takes the product (else the prefill kernel)
     int lora_stage;              // prefill: the item's xa rows staged in LDS (one split, 4 to 32 columns, aligned)
     const uint16_t* lora_b;      // B f16 [rows][lora_rank], the product's row order
     const int* lora_tab;         // module end rows (3 used), then each module's first column of xa (-1: none)
@@ -75,6 +76,7 @@ constexpr size_t PF_SK_PART_BYTES = (size_t)128 << 20;
 constexpr int PF_SK_ITEMS_MAX = 4096;
 // Cost of stream-K's partials in units of one group's compute (the launcher's choice between whole items and stream-K).
 constexpr int PF_SK_FIXUP = 12;
+constexpr double PF_SK_PIECE_S = 1e-6;  // stream-K fix-up: seconds per partial summed beyond three (measured)
 // K slices of plain prefill products (at most PF_KS_MAX, up to PF_KS_MAX_M tokens, slices x tokens at most PF_KS_ROWS
 // partial rows), and the estimated cost of a slice's extra pipeline start and partial, in the same units.
 constexpr int PF_KS_MAX = 16;
@@ -88,7 +90,9 @@ constexpr int PF_KS_COST = 2;
 constexpr double PF_KS_CU_FLOPS = 4e12, PF_KS_HBM = 5e12;
 
 // Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
-constexpr int SKINNY_MAX_M = 48;  // the skinny kernel up to 48 tokens (three 16-token blocks per MFMA pass)
+constexpr int SKINNY_MAX_M = 48;
+// plain symmetric int4 products of 33-48 tokens on matrices of at least this many weights take the prefill kernel
+constexpr size_t PF_FROM33_WEIGHTS = (size_t)1 << 26;  // the skinny kernel up to 48 tokens (three 16-token blocks per MFMA pass)
 // 16-row tiles per wave in the skinny kernel, and its pipeline depth (groups whose loads are in flight + 1).
 #ifndef QH_SKINNY_TILES
 #define QH_SKINNY_TILES 2

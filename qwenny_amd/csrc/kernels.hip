@@ -1252,7 +1252,14 @@ static long prefill_plan(Launch& l) {
     const size_t slot = (size_t)bm * wg_tiles * TILE * 4;
     const long sk = rounds >= 2 ? items - (rounds - 2) * P : items;
     const long U = sk * G;
-    const long fixup = l.stream_k > 1 ? l.stream_k : PF_SK_FIXUP;
+    // one group of one item on a CU running per_cu of them at PF_KS_CU_FLOPS (seconds)
+    const double unit_s = 2.0 * bm * wg_tiles * TILE * QG * per_cu / PF_KS_CU_FLOPS;
+    // the fix-up reads an item's partials one after another, so each piece beyond three adds PF_SK_PIECE_S: with q
+    // units per workgroup an item is cut in about ceil(G / q) pieces (measured: 64 x 128 items of 48 groups cut in
+    // 48 pieces took 48 us, in 16 pieces 31 us, against 13 and 19 us in 4 K slices)
+    const long q = std::max(1l, U / P), pieces = (G + q - 1) / q;
+    const long fixup = (l.stream_k > 1 ? l.stream_k : PF_SK_FIXUP) +
+                       (long)(std::max(0l, pieces - 3) * PF_SK_PIECE_S / unit_s + 0.5);
     const long t_sk = (rounds >= 2 ? (rounds - 2) * G : 0) + (U + P - 1) / P + fixup;
     if (t_sk * 20 < t_dp * 19 && 2 * P * slot <= PF_SK_PART_BYTES && sk <= PF_SK_ITEMS_MAX && U >= P &&
         items * G < (1l << 31)) {
@@ -1268,9 +1275,7 @@ static long prefill_plan(Launch& l) {
         for (int ks = 2; ks <= PF_KS_MAX && ks <= G && (ks <= 4 || G / ks >= PF_KS_MIN_G) && (long)ks * l.m <= PF_KS_ROWS;
              ks *= 2) {
             // the extra partials (ks - 1 more f32 outputs per token and row, written here and read back by the
-            // consumer) at PF_KS_HBM bytes/s, in units of one group of one item on a CU running per_cu of them at
-            // PF_KS_CU_FLOPS
-            const double unit_s = 2.0 * bm * wg_tiles * TILE * QG * per_cu / PF_KS_CU_FLOPS;
+            // consumer) at PF_KS_HBM bytes/s, in units of unit_s
             const double extra_s = (double)(ks - 1) * l.m * l.rows * 8 / PF_KS_HBM;
             const long units = items * ks,
                        t_ks = (units + P - 1) / P * ((G + ks - 1) / ks) + PF_KS_COST + (long)(extra_s / unit_s + 0.5);
@@ -1348,7 +1353,7 @@ static hipError_t prefill_epi(Launch& l) {
 // parallel, plus once with QH_PART_DISPATCH for the dispatcher.
 template <int F, int EPI>
 hipError_t launch_epi(Launch& l) {
-    if (l.m <= SKINNY_MAX_M) return l.dry_run ? hipSuccess : skinny_epi<F & ~F_PERCH, EPI>(l);
+    if (l.skinny) return l.dry_run ? hipSuccess : skinny_epi<F & ~F_PERCH, EPI>(l);
     return prefill_epi<F, EPI>(l);
 }
 template hipError_t launch_epi<QH_PART_F, QH_PART_EPI>(Launch& l);

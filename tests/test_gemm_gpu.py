@@ -35,12 +35,12 @@ def _plain(gemm, mat, x, m, stream=None):
     return y.sum(0).cpu().numpy().astype(np.float64)
 
 
-def _check(got, q, x, m):
-    """The bar against the oracle, and the kernel's own arithmetic to 1e-4."""
+def _check(got, q, x, kernel):
+    """The bar against the oracle, and the arithmetic of the kernel that ran (Mat.kernel) to 1e-4."""
     want = oracle_y(q, x)
     err = rel_err(got, want)
     assert err <= TOL, f"max|err|/rms {err:.3e} vs the oracle"
-    exact = want if m <= SKINNY_MAX_M else emulate_bf16_weights(q, x)
+    exact = want if kernel == "skinny" else emulate_bf16_weights(q, x)
     err = rel_err(got, exact)
     assert err <= 1e-4, f"max|err|/rms {err:.3e} vs the kernel's arithmetic"
 
@@ -54,7 +54,7 @@ def test_skinny_plain(gemm, kind, m):
     mat = Mat.stack(gemm, [q])
     assert mat.wt == WT_OF[kind]
     assert mat.per_channel == (kind == "i8")
-    _check(_plain(gemm, mat, x, m), q, x, m)
+    _check(_plain(gemm, mat, x, m), q, x, mat.kernel(m))
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -65,7 +65,7 @@ def test_prefill_plain(gemm, kind, m):
     x = activations(6 + m, "x", m, 768, outliers=0.01)
     mat = Mat.stack(gemm, [q])
     assert mat.per_channel == (kind == "i8")
-    _check(_plain(gemm, mat, x, m), q, x, m)
+    _check(_plain(gemm, mat, x, m), q, x, mat.kernel(m))
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -87,7 +87,7 @@ def test_silu(gemm, kind, m):
     assert gemm.run(None, m, mat, to_dev(x), y, Epi.Silu) == 1
     torch.cuda.synchronize()
     got = y.float().cpu().numpy()
-    if m <= SKINNY_MAX_M:
+    if mat.kernel(m, Epi.Silu) == "skinny":
         full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1)
         tol = TOL
     else:
@@ -150,6 +150,37 @@ def test_argmax_many_workgroups_repeated(gemm, n_out):
         assert rel_err(got, oracle_y(q, x)) <= TOL
 
 
+def test_kernel_switch_large_int4(gemm):
+    """Plain split-K products of 33-48 tokens on symmetric int4 matrices of at least 2^26 weights run on the prefill
+    kernel (its K slices are faster there); 32 tokens, whole products, the other epilogues, zero points and a matrix
+    one group of K short of 2^26 weights stay on the skinny kernel. Each side matches its own arithmetic (64 sampled
+    rows of a 4096 x 16384 matrix)."""
+    n, k = 4096, 16384
+    q = make_quant(180, "i4", n, k)
+    mat = Mat.stack(gemm, [q])
+    assert [mat.kernel(m) for m in (1, 32, 33, 48, 49)] == ["skinny", "skinny", "prefill", "prefill", "prefill"]
+    assert mat.kernel(40, whole=True) == "skinny" and mat.kernel(40, Epi.Argmax) == "skinny"
+    assert mat.kernel(40, Epi.Silu) == "skinny"
+    assert Mat.stack(gemm, [make_quant(181, "i4", n, k - 128)]).kernel(40) == "skinny"
+    assert Mat.stack(gemm, [make_quant(182, "i4z", n, k)]).kernel(40) == "skinny"
+    rows = np.sort(np.random.default_rng(3).choice(n, 64, replace=False))
+    sq = sub_quant(q, rows)
+    for m in (32, 33, 48):
+        print(f"kernel switch m={m}", flush=True)
+        x = activations(183 + m, "x", m, k, outliers=0.01)
+        split = mat.split(m)
+        got = _plain(gemm, mat, x, m)[:, rows]
+        _check(got, sq, x, mat.kernel(m))
+        assert m == 32 or 1 < split <= 16
+        if m == 33:  # the whole product on the skinny kernel: one partial, the split product's value
+            import torch
+
+            y = torch.full((1, m, n), float("nan"), dtype=torch.float32, device="cuda")
+            assert gemm.run_split(None, m, mat, to_dev(x), y, Epi.Plain, True) == 1
+            torch.cuda.synchronize()
+            _check(y[0].cpu().numpy().astype(np.float64)[:, rows], sq, x, "skinny")
+
+
 def test_argmax_rejects_too_many_rows(gemm):
     import torch
 
@@ -193,4 +224,4 @@ def test_small_and_odd_shapes(gemm, kind, n, k):
         q = make_quant(170 + m, kind, n, k)
         x = activations(171 + m, "x", m, k, outliers=0.01)
         mat = Mat.stack(gemm, [q])
-        _check(_plain(gemm, mat, x, m), q, x, m)
+        _check(_plain(gemm, mat, x, m), q, x, mat.kernel(m))

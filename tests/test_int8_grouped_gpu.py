@@ -85,7 +85,7 @@ def test_grouped_int8_plain(gemm, way, k, n, m):
     sq = sub_quant(q, rows)
     got = _plain(gemm, mat, x, m)[:, rows]
     want = oracle_y(sq, x)
-    if m <= SKINNY_MAX_M:
+    if mat.kernel(m) == "skinny":
         assert rel_err(got, want) <= 1e-4
     else:
         assert rel_err(got, want) <= TOL
@@ -117,7 +117,7 @@ def test_grouped_int8_silu(gemm, way, m):
     cols = np.sort(np.random.default_rng(m).choice(n, 256, replace=False))
     got = y.float().cpu().numpy()[:, cols]
     sg, su = sub_quant(gate, cols), sub_quant(up, cols)
-    if m <= SKINNY_MAX_M:
+    if mat.kernel(m, Epi.Silu) == "skinny":
         g, u = oracle_y(sg, x), oracle_y(su, x)
         tol = TOL
     else:
@@ -151,7 +151,7 @@ def test_grouped_int8_argmax(gemm, way, n_out):
     samp = np.sort(np.random.default_rng(1).choice(n, 512, replace=False))
     sq = sub_quant(q, samp)
     want = oracle_y(sq, x[rows])
-    if n_out <= SKINNY_MAX_M:
+    if mat.kernel(n_out, Epi.Argmax) == "skinny":
         assert rel_err(got[:, samp], want) <= 1e-4
     else:
         assert rel_err(got[:, samp], want) <= TOL

@@ -53,7 +53,7 @@ def test_marlin_rows_then_put_block(gemm, kind, m):
     assert (mat.rows, mat.valid, mat.wt) == (128, 32, Wt.I4Z if kind == "i4z" else Wt.I4)
     x = activations(9 + m, "x", m, k)
     got = _plain(gemm, mat, x, m)
-    tol = 1e-4 if m <= SKINNY_MAX_M else TOL
+    tol = 1e-4 if mat.kernel(m) == "skinny" else TOL
     assert rel_err(got[:, :32], oracle_y(sub_quant(q, first), x)) <= tol
     logits, keys = _argmax(gemm, mat, x)
     assert (keys == oracle.argmax_keys(logits, 32)).all()
@@ -97,8 +97,9 @@ def test_wide_groups(gemm, group, m):
     q = make_quant(74, "i4z", 256, 1024, group=group)
     assert q.group == group
     x = activations(11, "x", m, 1024)
-    got = _plain(gemm, Mat.stack(gemm, [q]), x, m)
-    assert rel_err(got, oracle_y(q, x)) <= (1e-4 if m <= SKINNY_MAX_M else TOL)
+    mat = Mat.stack(gemm, [q])
+    got = _plain(gemm, mat, x, m)
+    assert rel_err(got, oracle_y(q, x)) <= (1e-4 if mat.kernel(m) == "skinny" else TOL)
 
 
 @pytest.mark.parametrize("zp", [False, True])
@@ -114,7 +115,7 @@ def test_f32_scales(gemm, zp, m):
     mat = Mat.stack(gemm, [q2])
     assert mat.wt == (Wt.I4Z_S32 if zp else Wt.I4_S32)
     x = activations(12, "x", m, 512)
-    assert rel_err(_plain(gemm, mat, x, m), oracle_y(q2, x)) <= (1e-4 if m <= SKINNY_MAX_M else TOL)
+    assert rel_err(_plain(gemm, mat, x, m), oracle_y(q2, x)) <= (1e-4 if mat.kernel(m) == "skinny" else TOL)
 
 
 @pytest.mark.parametrize("m", [1, 4, 33])
@@ -127,8 +128,9 @@ def test_strided_activations(gemm, m):
     wide = activations(13, "x", m, ldx)
     x = wide[:, :k]
     xdev = torch.from_numpy(np.ascontiguousarray(wide).view(np.int16)).cuda().view(torch.bfloat16)
-    got = _plain(gemm, Mat.stack(gemm, [q]), x, m, ldx=ldx, xdev=xdev)
-    assert rel_err(got, oracle_y(q, np.ascontiguousarray(x))) <= (1e-4 if m <= SKINNY_MAX_M else TOL)
+    mat = Mat.stack(gemm, [q])
+    got = _plain(gemm, mat, x, m, ldx=ldx, xdev=xdev)
+    assert rel_err(got, oracle_y(q, np.ascontiguousarray(x))) <= (1e-4 if mat.kernel(m) == "skinny" else TOL)
 
 
 @pytest.mark.parametrize("kind", ["i4", "i8"])

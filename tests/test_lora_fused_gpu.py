@@ -68,7 +68,7 @@ def test_lora_plain_fused(gemm, m, rank, split, ends):
     assert np.array_equal(got[1:], plain[1:])
     assert np.array_equal(got[0][:, e0:e1], plain[0][:, e0:e1])
     xa, b, tab_h, tok_slot, slot_scale = host
-    base = oracle_y(q, x) if m <= SKINNY_MAX_M else emulate_bf16_weights(q, x)
+    base = oracle_y(q, x) if mat.kernel(m) == "skinny" else emulate_bf16_weights(q, x)
     want = oracle.lora_add(base, xa, split, b, rank, tab_h, tok_slot, slot_scale, m)
     assert rel_err(got.astype(np.float64).sum(0), want) <= 1e-4
     # against the unfused path on the same partials: the delta itself to f32 accuracy
@@ -99,7 +99,7 @@ def test_lora_silu_fused(gemm, m, rank, split, half, k):
     torch.cuda.synchronize()
     got = mid.float().cpu().numpy()
     order = row_order(rows, True)
-    full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1) if m <= SKINNY_MAX_M else \
+    full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1) if mat.kernel(m, Epi.Silu) == "skinny" else \
         np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
     packed = full[:, order]  # the product in its packed (SwiGLU) row order
     xa, b, tab_h, tok_slot, slot_scale = host

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from qwenny_amd import SKINNY_MAX_M, Epi, Mat, lora_add, lora_silu, row_order, sum_parts
+from qwenny_amd import Epi, Mat, lora_add, lora_silu, row_order, sum_parts
 from qwenny_amd.synth import activations, bf16_to_f32, f32_to_bf16
 from tests.helpers import bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, to_dev
 
@@ -98,7 +98,7 @@ def test_lora_add_end_to_end(gemm, m):
     bf = b.astype(np.float64)
     delta = np.concatenate([xs[:, :rank] @ bf[:512].T, xs[:, rank:] @ bf[512:].T], axis=1)
     # decode products are exact; prefill ones round each int4 weight to bf16 once (the same bar on that arithmetic)
-    base = oracle_y(q, x) if m <= SKINNY_MAX_M else emulate_bf16_weights(q, x)
+    base = oracle_y(q, x) if w.kernel(m) == "skinny" else emulate_bf16_weights(q, x)
     want = base + slot_scale[tok_slot][:, None] * delta
     assert rel_err(out.cpu().numpy(), want) <= 1e-4
 
