@@ -151,10 +151,10 @@ def test_argmax_many_workgroups_repeated(gemm, n_out):
 
 
 def test_kernel_switch_large_int4(gemm):
-    """Plain split-K products of 33-48 tokens on symmetric int4 matrices of at least 2^26 weights run on the prefill
-    kernel (its K slices are faster there); 32 tokens, whole products, the other epilogues, zero points and a matrix
-    one group of K short of 2^26 weights stay on the skinny kernel. Each side matches its own arithmetic (64 sampled
-    rows of a 4096 x 16384 matrix)."""
+    """Plain split-K products of 33-48 tokens on int4 and grouped int8 matrices of at least 2^26 weights run on the
+    prefill kernel (its K slices are faster there); 32 tokens, whole products, the other epilogues, per-channel int8
+    and a matrix one group of K short of 2^26 weights stay on the skinny kernel. Each side matches its own arithmetic
+    (64 sampled rows of 4096 x 16384 matrices, symmetric int4 and with zero points)."""
     n, k = 4096, 16384
     q = make_quant(180, "i4", n, k)
     mat = Mat.stack(gemm, [q])
@@ -162,9 +162,17 @@ def test_kernel_switch_large_int4(gemm):
     assert mat.kernel(40, whole=True) == "skinny" and mat.kernel(40, Epi.Argmax) == "skinny"
     assert mat.kernel(40, Epi.Silu) == "skinny"
     assert Mat.stack(gemm, [make_quant(181, "i4", n, k - 128)]).kernel(40) == "skinny"
-    assert Mat.stack(gemm, [make_quant(182, "i4z", n, k)]).kernel(40) == "skinny"
+    assert Mat.stack(gemm, [make_quant(183, "i8", n, k)]).kernel(40) == "skinny"
+    assert Mat.stack(gemm, [make_quant(184, "i8g", n, k)]).kernel(40) == "prefill"
+    qz = make_quant(182, "i4z", n, k)
+    zmat = Mat.stack(gemm, [qz])
+    assert zmat.kernel(40) == "prefill"
     rows = np.sort(np.random.default_rng(3).choice(n, 64, replace=False))
     sq = sub_quant(q, rows)
+    for m in (33, 48):
+        print(f"kernel switch zero points m={m}", flush=True)
+        x = activations(190 + m, "x", m, k, outliers=0.01)
+        _check(_plain(gemm, zmat, x, m)[:, rows], sub_quant(qz, rows), x, zmat.kernel(m))
     for m in (32, 33, 48):
         print(f"kernel switch m={m}", flush=True)
         x = activations(183 + m, "x", m, k, outliers=0.01)
