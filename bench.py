@@ -435,13 +435,14 @@ class SummedStep(Step):
 
 
 def short_prefill_line(gemm, set_mats, args):
-    """Plain int4 products of 64, 256 and 512 tokens on the 27B prefill shapes (K slices or stream-K, whichever the
-    launcher picks), in HIP graphs: TFLOP/s of the product alone, and of the product followed by the sum of its
+    """Plain int4 products of 40, 64, 256 and 512 tokens on the 27B prefill shapes (K slices or stream-K, whichever the
+    launcher picks; at 40 tokens (5120, 17408) and (17408, 5120) take the prefill kernel, (5120, 6144) the skinny
+    kernel), in HIP graphs: TFLOP/s of the product alone, and of the product followed by the sum of its
     partials (sum_parts, only when the split is above 1), with the split used."""
     from qwenny_amd import Epi
 
     out = {}
-    for m in (64, 256, 512):
+    for m in (40, 64, 256, 512):
         for i, (k, n) in enumerate(PREFILL_27B):
             mat = set_mats[[0, 2, 3][i]][0]
             alone = Step(gemm, m, k)

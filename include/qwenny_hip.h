@@ -182,8 +182,8 @@ int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n);
  * QH_KERNEL_SKINNY (exact products of the dequantized weights) or QH_KERNEL_PREFILL (weights rounded to bf16 once;
  * both within the bf16-operand bound). No counterpart in the reference, whose Marlin kernel serves every token count:
  * for callers and tests that need to know which numerics a product has. The skinny kernel takes up to 48 tokens,
- * except plain split-K products of int4 and grouped int8 matrices of at least 2^26 weights from 33 tokens. No
- * launch. */
+ * except split-K plain and SwiGLU products of int4 and grouped int8 matrices of at least 2^26 weights from 33
+ * tokens. No launch. */
 #define QH_KERNEL_SKINNY 1
 #define QH_KERNEL_PREFILL 2
 int qh_mat_kernel(const qh_ctx* ctx, const qh_mat* m, size_t n, int epi, int whole);

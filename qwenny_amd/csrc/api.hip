@@ -316,18 +316,19 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
 }
 
 // Whether the skinny kernel takes a product of m tokens (else the prefill kernel): up to SKINNY_MAX_M tokens, except
-// plain split-K products of int4 or grouped int8 matrices of at least PF_FROM33_WEIGHTS weights from 33 tokens (three
-// 16-token blocks per skinny wave), where the prefill kernel's K slices are faster (measured on the 27B shapes
-// (5120, 17408) and (17408, 5120) at 33-48 tokens: 1.10-1.29x per product for int4 with zero points, 1.17-1.27x
-// symmetric, 1.36-1.50x grouped int8, more with the partials summed; on the smaller 27B shapes, 31M weights, the
-// skinny kernel stays ahead). Per-channel int8 and bf16 matrices were not measured there and stay on the skinny kernel.
-// QH_PF_FROM (tuning) moves every plain product from that many tokens to the prefill kernel instead.
+// split-K plain and SwiGLU products of int4 or grouped int8 matrices of at least PF_FROM33_WEIGHTS weights from 33
+// tokens (three 16-token blocks per skinny wave), where the prefill kernel is faster (measured at 33-48 tokens on the
+// 27B shapes (5120, 17408) and (17408, 5120), plain: 1.10-1.29x per product for int4 with zero points, 1.17-1.27x
+// symmetric, 1.36-1.50x grouped int8, more with the partials summed; the [gate; up] SwiGLU product 1.14-1.36x; on
+// the smaller 27B shapes, 31M weights, the skinny kernel stays ahead). The argmax epilogue (the 27B head: 238 against
+// 254 us at 48 tokens), whole plain products, per-channel int8 and bf16 matrices stay on the skinny kernel.
+// QH_PF_FROM (tuning) moves every product from that many tokens to the prefill kernel instead.
 static bool use_skinny(const qh_ctx* ctx, const qh_mat* w, size_t m, int epi, int whole) {
     if (m > (size_t)SKINNY_MAX_M) return false;
-    if (epi != QH_EPI_PLAIN) return true;
     if (ctx->pf_from <= SKINNY_MAX_M) return m < (size_t)ctx->pf_from;
+    if (epi == QH_EPI_ARGMAX || (epi == QH_EPI_PLAIN && whole)) return true;
     const bool fmt = (!is_i8(w->wt) && !is_bf16(w->wt)) || (is_i8(w->wt) && !w->per_channel);
-    return !(m > 32 && !whole && fmt && w->rows * w->cols >= PF_FROM33_WEIGHTS);
+    return !(m > 32 && fmt && w->rows * w->cols >= PF_FROM33_WEIGHTS);
 }
 
 // The launch of a product of m tokens (epi, x, y and keys as qh_gemm takes them; `whole`: one partial).

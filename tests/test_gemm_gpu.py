@@ -151,16 +151,16 @@ def test_argmax_many_workgroups_repeated(gemm, n_out):
 
 
 def test_kernel_switch_large_int4(gemm):
-    """Plain split-K products of 33-48 tokens on int4 and grouped int8 matrices of at least 2^26 weights run on the
-    prefill kernel (its K slices are faster there); 32 tokens, whole products, the other epilogues, per-channel int8
-    and a matrix one group of K short of 2^26 weights stay on the skinny kernel. Each side matches its own arithmetic
-    (64 sampled rows of 4096 x 16384 matrices, symmetric int4 and with zero points)."""
+    """Split-K plain and SwiGLU products of 33-48 tokens on int4 and grouped int8 matrices of at least 2^26 weights run
+    on the prefill kernel (faster there); 32 tokens, whole products, the argmax, per-channel int8 and a matrix one
+    group of K short of 2^26 weights stay on the skinny kernel. Each side matches its own arithmetic (64 sampled rows
+    of 4096 x 16384 matrices, symmetric int4 and with zero points; a [gate; up] SwiGLU product of 2 x 2048 rows)."""
     n, k = 4096, 16384
     q = make_quant(180, "i4", n, k)
     mat = Mat.stack(gemm, [q])
     assert [mat.kernel(m) for m in (1, 32, 33, 48, 49)] == ["skinny", "skinny", "prefill", "prefill", "prefill"]
     assert mat.kernel(40, whole=True) == "skinny" and mat.kernel(40, Epi.Argmax) == "skinny"
-    assert mat.kernel(40, Epi.Silu) == "skinny"
+    assert mat.kernel(40, Epi.Silu) == "prefill" and mat.kernel(32, Epi.Silu) == "skinny"
     assert Mat.stack(gemm, [make_quant(181, "i4", n, k - 128)]).kernel(40) == "skinny"
     assert Mat.stack(gemm, [make_quant(183, "i8", n, k)]).kernel(40) == "skinny"
     assert Mat.stack(gemm, [make_quant(184, "i8g", n, k)]).kernel(40) == "prefill"
@@ -173,6 +173,25 @@ def test_kernel_switch_large_int4(gemm):
         print(f"kernel switch zero points m={m}", flush=True)
         x = activations(190 + m, "x", m, k, outliers=0.01)
         _check(_plain(gemm, zmat, x, m)[:, rows], sub_quant(qz, rows), x, zmat.kernel(m))
+    import torch
+
+    gate, up = make_quant(185, "i4", n // 2, k), make_quant(186, "i4", n // 2, k)
+    gu = Mat.stack(gemm, [gate, up], silu=True)
+    half = np.sort(np.random.default_rng(4).choice(n // 2, 32, replace=False))
+    for m in (32, 40):
+        print(f"kernel switch SwiGLU m={m}", flush=True)
+        x = activations(195 + m, "x", m, k)
+        y = torch.full((m, n // 2), float("nan"), dtype=torch.bfloat16, device="cuda")
+        assert gemm.run(None, m, gu, to_dev(x), y, Epi.Silu) == 1
+        torch.cuda.synchronize()
+        # output column j is silu(gate row j) * up row j
+        sg, su = sub_quant(gate, half), sub_quant(up, half)
+        if gu.kernel(m, Epi.Silu) == "skinny":
+            g, u, tol = oracle_y(sg, x), oracle_y(su, x), TOL
+        else:
+            g, u, tol = emulate_bf16_weights(sg, x), emulate_bf16_weights(su, x), 1e-3
+        want = oracle.silu_glu(np.concatenate([g, u], axis=1), None)
+        assert bf16_out_err(y.float().cpu().numpy()[:, half], want) <= tol
     for m in (32, 33, 48):
         print(f"kernel switch m={m}", flush=True)
         x = activations(183 + m, "x", m, k, outliers=0.01)
@@ -181,8 +200,6 @@ def test_kernel_switch_large_int4(gemm):
         _check(got, sq, x, mat.kernel(m))
         assert m == 32 or 1 < split <= 16
         if m == 33:  # the whole product on the skinny kernel: one partial, the split product's value
-            import torch
-
             y = torch.full((1, m, n), float("nan"), dtype=torch.float32, device="cuda")
             assert gemm.run_split(None, m, mat, to_dev(x), y, Epi.Plain, True) == 1
             torch.cuda.synchronize()
