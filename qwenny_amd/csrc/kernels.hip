@@ -1329,11 +1329,15 @@ static hipError_t prefill_epi(Launch& l) {
         if (l.m > 128 && (waves2 >= 4 * l.cus || (waves2 >= 2 * l.cus && l.cols / QG >= 64)) && pads_ok(256)) {
             shape = 2;
             // 256 x 192 on 12 waves when its rounds fill the CUs enough better to outweigh its lower rate (items of
-            // 3/4 the work at about 0.85 of the rate of 256 x 256: (5120, 6144) at 2048 tokens fills all 256 CUs with
-            // it, 3/4 of them with 256 x 256, measured +10%)
+            // 3/4 the work at about 0.85 of the rate of 256 x 256), and only where 256 x 256 items would fill at most
+            // 5/8 of the CUs: beside the ping-pong 256 x 256 kernel it won only up to there (measured at 768-4096
+            // tokens: at 50-62.5% fill +2-11%, e.g. (2560, 4096) at 2048, (5120, 10240) at 1024, (6144, 5120) at
+            // 2048; at 75-150% fill, (5120, 6144) at 2048 and 4096 tokens, it lost 3-6%)
             Launch a = l, b = l;
             a.dry_run = b.dry_run = 1;
-            if (prefill_plan<F, EPI, 4, 1, 2, 6>(a) * 15 < prefill_plan<F, EPI, 8, 1, 1, 8>(b) * 17) shape = 7;
+            if (items(256, 16) * 8 <= (long)l.cus * 5 &&
+                prefill_plan<F, EPI, 4, 1, 2, 6>(a) * 15 < prefill_plan<F, EPI, 8, 1, 1, 8>(b) * 17)
+                shape = 7;
         } else if (l.m > 64 && items(128, 8) * 4 >= l.cus && pads_ok(128)) shape = 5;
         else shape = 6;
     }
