@@ -280,7 +280,7 @@ def dense_lines(gemm, args):
     k, n = shapes[0]
     pst = Step(gemm, 2048, k)
     pst.add(mats[0][0], Epi.Plain, k * n * 2 + 2048 * (k + n) * 2, 2 * 2048 * k * n)
-    msp = time_step(pst, max(10, args.steps // 10), 3, False)
+    msp = time_step(pst, max(10, args.steps // 10), 3, not args.no_graph)
     out["bf16_dense_prefill_m2048_TFLOPs"] = round(pst.flops() / (msp * 1e-3) / 1e12, 1)
     a = torch.randn(2048, k, device="cuda").to(torch.bfloat16)
     b = torch.randn(n, k, device="cuda").to(torch.bfloat16)
@@ -558,7 +558,7 @@ def grouped_int8_line(gemm, args):
     for ms_, (k, n) in zip(mats, shapes):
         stp = Step(gemm, 2048, k)
         stp.add(ms_[0], Epi.Plain, gbytes(k, n, 2048), 2 * 2048 * k * n)
-        msp = time_step(stp, max(10, args.steps // 10), 3, False)
+        msp = time_step(stp, max(10, args.steps // 10), 3, not args.no_graph)
         out[f"m2048_{k}x{n}_TFLOPs"] = round(stp.flops() / (msp * 1e-3) / 1e12, 1)
     print(f"# grouped int8: {out}", file=sys.stderr, flush=True)
     return {"int8_grouped": out}
@@ -579,7 +579,7 @@ def prefill_zp_line(gemm, args):
         st.x = torch.from_numpy(activations(671, "x", 2048, k, outliers=0.01).view(np.int16)).cuda().view(
             torch.bfloat16)
         st.add(mat, Epi.Plain, int4_bytes(k, n, 2048, zp=True), 2 * 2048 * k * n)
-        msp = time_step(st, max(10, args.steps // 10), 3, False)
+        msp = time_step(st, max(10, args.steps // 10), 3, not args.no_graph)
         out[f"{k}x{n}"] = round(st.flops() / (msp * 1e-3) / 1e12, 1)
     print(f"# prefill M=2048 with zero points: {out} TFLOP/s", file=sys.stderr, flush=True)
     return {"prefill_zp_m2048_TFLOPs": out}
@@ -756,7 +756,7 @@ def main():
             mat = set_mats[[0, 2, 3][i]][0]
             st = Step(gemm, 2048, k)
             st.add(mat, Epi.Plain, int4_bytes(k, n, 2048), 2 * 2048 * k * n)
-            msp = time_step(st, max(10, args.steps // 10), 3, False)
+            msp = time_step(st, max(10, args.steps // 10), 3, not args.no_graph)
             tf = st.flops() / (msp * 1e-3) / 1e12
             pf[f"{k}x{n}"] = round(tf, 1)
             print(f"# prefill M=2048 K={k} N={n}: {msp:.3f} ms, {tf:.1f} TFLOP/s ({tf / BF16_PEAK:.1%})",
@@ -784,7 +784,7 @@ def main():
         for mats, (k, n) in zip(i8, [(5120, 17408), (17408, 5120)]):
             stp = Step(gemm, 2048, k)
             stp.add(mats[0], Epi.Plain, int8_bytes(k, n, 2048), 2 * 2048 * k * n)
-            msp = time_step(stp, max(10, args.steps // 10), 3, False)
+            msp = time_step(stp, max(10, args.steps // 10), 3, not args.no_graph)
             pf8[f"{k}x{n}"] = round(stp.flops() / (msp * 1e-3) / 1e12, 1)
         extra["int8_prefill_m2048_TFLOPs"] = pf8
         print(f"# int8 M=5: {ms85:.4f} ms/step, {extra['int8_m5_GBps']} GB/s; M=2048: {pf8} TFLOP/s",
