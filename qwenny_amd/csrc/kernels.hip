@@ -352,7 +352,7 @@ __host__ __device__ constexpr bool skinny_wave_x(int m, int fmt, int ng) {
 }
 
 template <int F, int EPI, int NR, int T, int NG, int TB>
-__global__ __launch_bounds__(TB == 1 ? 1024 : 512) void skinny_kernel(Launch a) {
+__global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu(NG == 1 && TB > 1 ? 4 : 1))) void skinny_kernel(Launch a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int CW = CodeWords<F>::N;
     // the workgroup is WT wave columns (x) by WK wave rows (y): no division in the index set-up, which every wave
