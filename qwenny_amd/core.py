@@ -18,9 +18,11 @@ from ._lib import MatDesc, QuantC, check, lib
 P = ctypes.c_void_p
 
 
-# Token counts the decode (skinny) kernel takes: its products are exact (every weight bf16 (128 + q) times x summed in
-# f32, the scale after), and plain ones return split-K partials; above it the prefill kernel rounds each dequantized
-# weight to bf16 once and plain products return one partial (csrc/kernels.h SKINNY_MAX_M).
+# Token counts the decode (skinny) kernel takes at most (csrc/kernels.h SKINNY_MAX_M; from 33 tokens the plain and
+# SwiGLU products of int4 and grouped int8 matrices of 2^26 weights or more go to the prefill kernel instead:
+# Mat.kernel says which kernel a product runs on). The skinny kernel's products are exact (every weight bf16 (128 + q)
+# times x summed in f32, the scale after) and plain ones return split-K partials; the prefill kernel rounds each
+# dequantized weight to bf16 once, and its plain products return 1-16 partials (K slices) up to 512 tokens, one above.
 SKINNY_MAX_M = 48
 
 

@@ -1,4 +1,5 @@
-// Device side of the C ABI (include/qwenny_hip.h): contexts, device matrices and the product dispatch by token count.
+// Device side of the C ABI (include/qwenny_hip.h): contexts, device matrices and the product dispatch by token count
+// (and, at 33-48 tokens, matrix size).
 // Mirrors the reference's Gemm / Mat runtime (cuda/core.rs:94-681) over HIP: the matrix owns its device buffers, the
 // product only launches (no allocation, no host synchronisation), errors come back as status codes.
 #include <hip/hip_runtime.h>

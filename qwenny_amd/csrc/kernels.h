@@ -89,10 +89,11 @@ constexpr int PF_KS_COST = 2;
 // The rates that price the slices' extra partials in those units: one CU's MFMA rate under load, and HBM.
 constexpr double PF_KS_CU_FLOPS = 4e12, PF_KS_HBM = 5e12;
 
-// Tokens the skinny kernel takes at most; larger steps go to the prefill kernel.
+// Tokens the skinny kernel takes at most (three 16-token blocks per MFMA pass); larger steps go to the prefill kernel.
 constexpr int SKINNY_MAX_M = 48;
-// plain and SwiGLU int4 and grouped int8 products of 33-48 tokens on matrices of at least this many weights take the prefill kernel
-constexpr size_t PF_FROM33_WEIGHTS = (size_t)1 << 26;  // the skinny kernel up to 48 tokens (three 16-token blocks per MFMA pass)
+// Split-K plain and SwiGLU products of 33-48 tokens on int4 and grouped int8 matrices of at least this many weights
+// take the prefill kernel (faster there; api.hip use_skinny).
+constexpr size_t PF_FROM33_WEIGHTS = (size_t)1 << 26;
 // 16-row tiles per wave in the skinny kernel, and its pipeline depth (groups whose loads are in flight + 1).
 #ifndef QH_SKINNY_TILES
 #define QH_SKINNY_TILES 2

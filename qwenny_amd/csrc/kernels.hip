@@ -6,7 +6,8 @@
 // B 32 k x 16 outputs; lane l of a wave holds D[token 4 (l / 16) + r][output l % 16], r = 0..3), the prefill kernel
 // v_mfma_f32_32x32x16_bf16 (its layout below).
 //
-// skinny_kernel (m <= 48, decode, MTP verify and small batches): HBM-bound. The weights are streamed once with 16-byte loads (a wave
+// skinny_kernel (m <= 48, decode, MTP verify and small batches; from 33 tokens not the plain and SwiGLU products of
+// matrices of 2^26 weights and more, which the prefill kernel takes): HBM-bound. The weights are streamed once with 16-byte loads (a wave
 // reads each (tile, group) block as one contiguous KiB) and turned into bf16 (128 + q) with one and-or per two values;
 // the MFMA sums x (128 + q) exactly in f32 per 128-column group, and the group's scale and zero point are applied
 // after it: acc += s (D - (128 + z) sum_k x), where sum_k x comes from one more MFMA against ones per k32 step (shared
@@ -14,7 +15,7 @@
 // the grid (the split-K partials of the output contract). The activations are staged in LDS once per workgroup, or,
 // for one token of int4 without zero points, by each wave for itself (no workgroup barrier).
 //
-// prefill_kernel (m > 48): MFMA-bound. A workgroup computes up to 256 tokens x 256 outputs (8 waves of 256 x 32, or
+// prefill_kernel (m > 48, and those 33-48-token products): MFMA-bound. A workgroup computes up to 256 tokens x 256 outputs (8 waves of 256 x 32, or
 // 256 x 192 on 12 waves of 128 x 32, or smaller tiles for short steps); the activation tile goes global -> LDS directly
 // (global_load_lds) into double-buffered, XOR-swizzled 64-column stages, each wave dequantizes its own outputs'
 // weights straight from global memory into bf16 registers ((q - z) s in f32, rounded once), the workgroups are mapped
