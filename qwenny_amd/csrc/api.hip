@@ -31,7 +31,7 @@ struct qh_ctx {
     void* sk_scratch;
     int stream_k;
     int skinny_plain_wk;    // skinny kernel, plain products: wave rows over K per workgroup (1; QH_SKINNY_PLAIN_WK)
-    int pf_from;            // plain products from this many tokens take the prefill kernel (QH_PF_FROM, tuning)
+    int pf_from;            // products from this many tokens take the prefill kernel (QH_PF_FROM, tuning; 49: off)
 };
 
 int qh::ctx_device(const qh_ctx* ctx) { return ctx->device; }
