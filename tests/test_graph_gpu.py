@@ -23,8 +23,10 @@ def test_graph_replays_match_eager(gemm):
     head = Mat.stack(gemm, [make_quant(92, "i4z", 8192, k)])     # skinny, argmax across workgroups
     pre = Mat.stack(gemm, [make_quant(93, "i4", 4096, k)])       # prefill at 256 tokens: items spread (stream-K)
     sl = Mat.stack(gemm, [make_quant(94, "i4", 1024, k)])        # prefill at 64 tokens: K-sliced partials
-    m_dec, m_pre, m_sl = 1, 256, 64
-    assert sl.split(m_sl) > 1
+    big = Mat.stack(gemm, [make_quant(95, "i4", 16384, k)])      # 2^26 weights at 40 tokens: prefill, K-sliced
+    m_dec, m_pre, m_sl, m_big = 1, 256, 64, 40
+    assert sl.split(m_sl) > 1 and big.kernel(m_big) == "prefill" and big.split(m_big) > 1
+    y_big = torch.empty((big.split(m_big), m_big, big.rows), dtype=torch.float32, device="cuda")
     x_dec = torch.empty((m_dec, k), dtype=torch.bfloat16, device="cuda")
     x_pre = torch.empty((m_pre, k), dtype=torch.bfloat16, device="cuda")
     y_sl = torch.empty((sl.split(m_sl), m_sl, sl.rows), dtype=torch.float32, device="cuda")
@@ -39,10 +41,11 @@ def test_graph_replays_match_eager(gemm):
         gemm.run(stream, m_dec, head, x_dec, y_head, Epi.Argmax, n_out=m_dec, keys=keys)
         gemm.run(stream, m_pre, pre, x_pre, y_pre, Epi.Plain)
         gemm.run(stream, m_sl, sl, x_pre, y_sl, Epi.Plain)  # the first 64 tokens of x_pre
+        gemm.run(stream, m_big, big, x_pre, y_big, Epi.Plain)  # the first 40
 
     def outputs():
         return y_dec.sum(0).cpu().numpy(), y_head.cpu().numpy(), keys.cpu().numpy().view(np.uint64).copy(), \
-            y_pre.cpu().numpy(), y_sl.cpu().numpy()
+            y_pre.cpu().numpy(), y_sl.cpu().numpy(), y_big.cpu().numpy()
 
     def load_inputs(seed):
         x_dec.copy_(to_dev(activations(seed, "x", m_dec, k)))
@@ -69,6 +72,7 @@ def test_graph_replays_match_eager(gemm):
         y_head.fill_(float("nan"))
         y_pre.fill_(float("nan"))
         y_sl.fill_(float("nan"))
+        y_big.fill_(float("nan"))
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
