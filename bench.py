@@ -193,15 +193,22 @@ def load_traffic(name):
 
 def traffic_run(gemm, set_mats, steps=5):
     """The workload of the rocprofv3 --pmc passes: the roofline kernel's launches (27B set at M=1, plain, no graph)
-    and a plain torch copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES) that calibrates the counters."""
+    and two calibrations of the counters over COPY_BYTES: a plain torch copy (reads and writes COPY_BYTES) and
+    qh_diag_read's contiguous pass (reads COPY_BYTES with the decode kernel's own non-temporal 16-byte loads)."""
     import torch
 
     from qwenny_amd import Epi
+
+    from qwenny_amd.core import diag_read
 
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
+    # the read-only kernel with the decode kernel's own 16-byte non-temporal loads over the same known bytes
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for _ in range(3):
+        diag_read(None, src, COPY_BYTES >> 10, 1, 0, sink)
     st = Step(gemm, 1, 17408)
     for c in range(4):
         for mats, (k, n) in zip(set_mats, SET_27B):
@@ -227,8 +234,9 @@ def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
                 if r["Counter_Name"] != counter:
                     continue
                 name = r["Kernel_Name"]
-                kind = "copy" if ("copy" in name.lower() and "skinny" not in name) else (
-                    "skinny" if "skinny_kernel" in name else None)
+                kind = "diag" if "diag_read_kernel" in name else (
+                    "copy" if ("copy" in name.lower() and "skinny" not in name) else (
+                        "skinny" if "skinny_kernel" in name else None))
                 if kind:
                     out.setdefault(kind, []).append(float(r["Counter_Value"]))
         return out
@@ -237,17 +245,89 @@ def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
     mean = lambda v: sum(v) / len(v)
     # the copy: the largest readings are the full copies (torch may launch small copies too)
     fcopy, wcopy = max(fetch["copy"]), max(write["copy"])
-    ffac, wfac = COPY_BYTES / (fcopy * 1024), COPY_BYTES / (wcopy * 1024)
+    cfac, wfac = COPY_BYTES / (fcopy * 1024), COPY_BYTES / (wcopy * 1024)
+    # the fetch scale from the read with the skinny kernel's own loads (the torch copy's, beside it, cross-checks it)
+    fdiag = max(fetch["diag"]) if fetch.get("diag") else None
+    ffac = COPY_BYTES / (fdiag * 1024) if fdiag else cfac
     fk, wk = mean(fetch["skinny"]) * 1024 * ffac, mean(write["skinny"]) * 1024 * wfac
     res = {"kernel": "skinny_kernel int4 M=1, 27B layer set (5 shapes x 4 copies)",
            "fetch_kib_per_dispatch": mean(fetch["skinny"]), "write_kib_per_dispatch": mean(write["skinny"]),
            "copy_fetch_kib": fcopy, "copy_write_kib": wcopy, "copy_bytes": COPY_BYTES,
+           "diag_read_fetch_kib": fdiag, "copy_fetch_scale": cfac,
            "fetch_scale": ffac, "write_scale": wfac, "traffic_bytes_per_launch": round(fk + wk),
            "fetch_bytes_per_launch": round(fk), "write_bytes_per_launch": round(wk)}
     os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
     with open(os.path.join(ROOT, "profiles", f"{out_name}_traffic.json"), "w") as f:
         json.dump(res, f, indent=1)
     print(json.dumps(res))
+
+
+class ReadStep:
+    """The read floor of the roofline launches: qh_diag_read's tile-layout pass (pattern 1: the one-token plain
+    product's loads, partition and block walk) over buffers the size of each matrix's codes, replayable like Step."""
+
+    def __init__(self, shapes, copies):
+        import torch
+
+        self.bufs = [(torch.empty(k * n // 2, dtype=torch.uint8, device="cuda"), n // 16, k // 128)
+                     for _ in range(copies) for k, n in shapes]
+        self.sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.launches = self.bufs
+
+    def run(self, stream=None):
+        from qwenny_amd.core import diag_read
+
+        for buf, tiles, groups in self.bufs:
+            diag_read(stream, buf, tiles, groups, 1, self.sink)
+
+
+def read_floor(set_mats, args):
+    """Per launch, the time a read-only pass with the plain M=1 product's own loads and partition takes over the same
+    code bytes (no activations, scales, arithmetic or stores): the floor a product launch cannot go under on this part
+    (its launch and ramp included)."""
+    st = ReadStep(SET_27B, 4)
+    ms = time_step(st, args.steps, args.warmup, not args.no_graph)
+    per = ms * 1e-3 / len(st.launches)
+    code = sum(k * n // 2 for k, n in SET_27B) / len(SET_27B)
+    shapes = {}
+    for k, n in SET_27B[1:]:
+        one = ReadStep([(k, n)], 4)
+        shapes[f"{k}x{n}"] = round(time_step(one, args.steps, args.warmup, not args.no_graph) * 1e3 / 4, 3)
+    algo = sum(int4_bytes(k, n, 1) for k, n in SET_27B) / len(SET_27B)
+    out = {"us_per_launch": round(per * 1e6, 3), "code_GBps": round(code / per / 1e9, 1),
+           "frac_at_algorithmic_bytes": round(algo / per / 1e9 / HBM_PEAK, 4), "us_per_shape": shapes}
+    print(f"# read floor (diag read, the M=1 product's loads over its code bytes): {per * 1e6:.2f} us per launch, "
+          f"{code / per / 1e9:.1f} GB/s of codes; per shape {shapes} us", file=sys.stderr, flush=True)
+    return out
+
+
+CLOCK_NAME = "prefill_i4_m2048_27b_clock_mfma_busy"
+
+
+def load_clock(name=CLOCK_NAME):
+    """The committed rocprofv3 clock / MFMA-busy summary of the prefill kernels, if there is one."""
+    p = os.path.join(ROOT, "profiles", f"{name}.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return None
+
+
+def roofline_prefill(extra):
+    """The MFMA half of the metric: the int4 prefill kernel at M=2048 on (5120, 17408), plain, symmetric; achieved
+    TFLOP/s from this run's HIP-event timing, MFMA busy and clock from the committed profile of the same launch."""
+    tf = extra["prefill_m2048_TFLOPs"]["5120x17408"]
+    flops = 2 * 2048 * 5120 * 17408
+    out = {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK, "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK, 4),
+           "kernel": "prefill_kernel<int4, plain> 256 x 256 items (ping-pong), M=2048, (K, N) = (5120, 17408)",
+           "flops_per_launch": flops, "us_per_launch": round(flops / (tf * 1e12) * 1e6, 2)}
+    clk = load_clock()
+    if clk:
+        row = clk.get("5120x17408")
+        if row:
+            out.update({"profile_us_per_launch": row["us"], "profile_clock_GHz": row["clock_GHz"],
+                        "mfma_busy": row["mfma_busy"]})
+    return out
 
 
 def dense_weights(seed, n, k):
@@ -613,6 +693,24 @@ def summarize_clock(pmc_dir, min_ns=50000):
         n = len(v)
         print(f"| `{name}` | {grid} | {n} | {sum(x[0] for x in v) / n / 1e3:.1f} | {sum(x[1] for x in v) / n:.2f} | "
               f"{sum(x[2] for x in v) / n:.3f} |")
+    # the --prefill-run workload launches the int4 prefill kernel 5 times per PREFILL_27B shape, in that order: the
+    # per-shape figures the bench's roofline_prefill reads (profiles/<CLOCK_NAME>.json)
+    pf = sorted((key[1], key) for key, (name, _, du) in meta.items() if "prefill_kernel" in name and du >= min_ns)
+    if len(pf) == 5 * len(PREFILL_27B):
+        out = {}
+        for i, (k, n) in enumerate(PREFILL_27B):
+            v = []
+            for _, key in pf[5 * i:5 * i + 5]:
+                cnt, du = per[key], meta[key][2]
+                cyc = cnt["GRBM_GUI_ACTIVE"] / 8
+                v.append((du, cyc / du, cnt.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / 1024 / cyc))
+            out[f"{k}x{n}"] = {"us": round(sum(x[0] for x in v) / 5 / 1e3, 2),
+                               "clock_GHz": round(sum(x[1] for x in v) / 5, 3),
+                               "mfma_busy": round(sum(x[2] for x in v) / 5, 4),
+                               "TFLOPs": round(2 * 2048 * k * n / (sum(x[0] for x in v) / 5 * 1e-9) / 1e12, 1)}
+        with open(os.path.join(ROOT, "profiles", f"{CLOCK_NAME}.json"), "w") as f:
+            json.dump(out, f, indent=1)
+        print(json.dumps(out))
 
 
 def main():
@@ -721,6 +819,8 @@ def main():
           f"{per_launch_bytes / per_launch_s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 
     extra = {}
+    floor = read_floor(set_mats, args)
+    extra["read_floor"] = floor
     if "m1sum" in only:
         # the same step with each plain product's split-K partials summed (sum_parts, one launch after each): what a
         # caller that needs whole rows pays on top of the products, over the same algorithmic bytes
@@ -830,6 +930,10 @@ def main():
                      "bytes_per_launch": round(per_launch_bytes), "us_per_launch": round(per_launch_s * 1e6, 3)},
         "extra": extra,
     }
+    line["roofline"]["read_floor_us_per_launch"] = floor["us_per_launch"]
+    line["roofline"]["frac_of_read_floor"] = round(floor["us_per_launch"] / (per_launch_s * 1e6), 4)
+    if "prefill" in only:
+        line["roofline_prefill"] = roofline_prefill(extra)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -278,6 +278,16 @@ int qh_lora_silu(void* stream, const float* xa, int split, int m_cols, const uin
                  const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n, const float* y,
                  size_t ldy, void* mid_bf16);
 
+/* ---- measurement aid ------------------------------------------------------------------------------------------ */
+
+/* No counterpart in the reference: a read-only kernel for the benchmark and its profiles. It reads `tiles` x `groups`
+ * 1 KiB blocks at buf (device, 16-byte aligned) with the decode kernel's 16-byte non-temporal loads and stores
+ * nothing (sink: device u32 scratch, never written in practice). pattern 0: contiguous, 8 KiB per wave (tiles x
+ * groups a multiple of 32; the FETCH_SIZE calibration); pattern 1: the tile-layout walk and partition of the
+ * one-token plain product (2 tiles x 4 groups per wave; tiles even, groups a multiple of 4; the read floor of a
+ * product over the same code bytes). Launch only. */
+int qh_diag_read(void* stream, const void* buf, size_t tiles, size_t groups, int pattern, uint32_t* sink);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,7 @@ SIGNATURES = {
     "qh_mat_dense": (I, [P, P, S, S, I, ctypes.POINTER(P)]),
     "qh_quant_to_bf16": (I, [ctypes.POINTER(QuantC), P]),
     "qh_dequant": (I, [P, P, P, P, S, S, S, I, I, S, S, P, I]),
+    "qh_diag_read": (I, [P, P, S, S, I, P]),
     "qh_sum_parts": (I, [P, P, I, S, S, P]),
     "qh_add_rmsnorm": (I, [P, P, P, I, S, S, P, P, ctypes.c_float]),
     "qh_lora_add": (I, [P, P, I, I, P, I, S, P, P, P, S, P, S]),

@@ -391,6 +391,12 @@ def dequant(stream, q, scales, zeros, rows, words, cols, group, bits, r0, n, out
                            n, _ptr(out), int(out_f32)))
 
 
+def diag_read(stream, buf, tiles, groups, pattern, sink):
+    """The measurement aid qh_diag_read: a read-only pass over tiles x groups 1 KiB blocks of `buf` with the decode
+    kernel's loads (pattern 0 contiguous, 1 the one-token product's tile walk), storing nothing; `sink` a device u32."""
+    check(lib().qh_diag_read(_stream(stream), _ptr(buf), tiles, groups, int(pattern), _ptr(sink)))
+
+
 def sum_parts(stream, x, splits, n, ld, y):
     """y [n][ld] = the sum of a plain product's `splits` partials x [splits][n][ld] (kernels/qwen.cu:141-143)."""
     check(lib().qh_sum_parts(_stream(stream), _ptr(x), splits, n, ld, _ptr(y)))

@@ -27,7 +27,8 @@ struct qh_ctx {
     int skinny_tile_waves;  // skinny kernel, plain products: waves side by side over tiles (0: by token count)
     int pf_shape;           // prefill workgroup shape (0: by tail waste; QH_PF_SHAPE for tuning sweeps)
     // prefill stream-K: partial tiles, then PF_SK_ITEMS_MAX item counters (zeroed here, left zero by every launch);
-    // QH_PF_SK=0 turns it off, a value above 1 replaces the launcher's fix-up cost (tuning)
+    // QH_PF_SK=0 turns it off, a value above 1 replaces the launcher's fix-up cost (tuning); then the f16 activations
+    // of prefill launches with f16 operands (X16_SCRATCH_BYTES)
     void* sk_scratch;
     int stream_k;
     int skinny_plain_wk;    // skinny kernel, plain products: wave rows over K per workgroup (1; QH_SKINNY_PLAIN_WK)
@@ -35,6 +36,11 @@ struct qh_ctx {
 };
 
 int qh::ctx_device(const qh_ctx* ctx) { return ctx->device; }
+
+// The context's own launch scratch.
+static Scratch ctx_scratch(const qh_ctx* ctx) {
+    return Scratch{ctx->argmax_scratch, ctx->sk_scratch, (uint8_t*)ctx->sk_scratch + PF_SK_SCRATCH_BYTES};
+}
 
 static int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
@@ -77,7 +83,7 @@ extern "C" int qh_open(int device, qh_ctx** out) {
         return fail(QH_EHIP, "argmax scratch: clear failed");
     }
     void* sk = nullptr;
-    const size_t sk_bytes = PF_SK_SCRATCH_BYTES;
+    const size_t sk_bytes = PF_SK_SCRATCH_BYTES + X16_SCRATCH_BYTES;
     if (hipMalloc(&sk, sk_bytes) != hipSuccess) {
         (void)hipFree(scratch);
         return fail(QH_ENOMEM, "prefill scratch of %zu bytes: allocation failed", sk_bytes);
@@ -362,6 +368,9 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
     l.pf_shape = ctx->pf_shape;
     l.sk_part = (float*)sc.stream_k;
     l.sk_count = (unsigned*)((uint8_t*)sc.stream_k + PF_SK_PART_BYTES);
+    l.x16 = sc.x16;
+    l.x16_bytes = X16_SCRATCH_BYTES;
+    l.lora_ldm = (int)m;
     l.stream_k = ctx->stream_k;
     l.nib_mask = 0x000F000Fu;
     l.ks = 1;
@@ -390,7 +399,7 @@ extern "C" int qh_mat_split(const qh_ctx* ctx, const qh_mat* m, size_t n) {
     if (use_skinny(ctx, m, n, QH_EPI_PLAIN, 0)) return skinny_partition(ctx, m, n, true).split;
     if (n > (size_t)PF_KS_MAX_M || n > (1u << 24)) return 1;
     Launch l = make_launch(ctx, m, nullptr, m->cols, n, nullptr, nullptr, QH_EPI_PLAIN, nullptr, 0, nullptr,
-                           Scratch{ctx->argmax_scratch, ctx->sk_scratch});
+                           ctx_scratch(ctx));
     l.dry_run = 1;
     if (hipError_t e = launch(l); e != hipSuccess) return fail(QH_EHIP, "split: %s", hipGetErrorString(e));
     return l.split;
@@ -406,10 +415,14 @@ extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size
     size_t len = 0;
     for (size_t i = 0; ctx && mats && i < count; i++) {
         if (!mats[i]) continue;
-        // decode sizes: the skinny partition's split (the same for every token count); prefill sizes up to
-        // PF_KS_MAX_M tokens: at most PF_KS_MAX partials and PF_KS_ROWS partial rows; beyond: one
-        size_t rows = std::max({max_tok, (size_t)qh_mat_split(ctx, mats[i], 1) * std::min(max_tok, (size_t)SKINNY_MAX_M),
-                                std::min((size_t)PF_KS_MAX * std::min(max_tok, (size_t)PF_KS_MAX_M), (size_t)PF_KS_ROWS)});
+        // decode sizes: the largest split x tokens over every token count the skinny kernel takes (its partition
+        // can depend on the token count, e.g. under QH_SKINNY_PLAIN_WK); prefill sizes up to PF_KS_MAX_M tokens: at
+        // most PF_KS_MAX partials and PF_KS_ROWS partial rows; beyond: one
+        size_t rows = std::max(max_tok, std::min((size_t)PF_KS_MAX * std::min(max_tok, (size_t)PF_KS_MAX_M),
+                                                 (size_t)PF_KS_ROWS));
+        for (size_t n = 1; n <= std::min(max_tok, (size_t)SKINNY_MAX_M); n++)
+            if (use_skinny(ctx, mats[i], n, QH_EPI_PLAIN, 0))
+                rows = std::max(rows, (size_t)skinny_partition(ctx, mats[i], n, true).split * n);
         len = std::max(len, rows * mats[i]->rows);
     }
     return len;
@@ -464,14 +477,14 @@ extern "C" int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x
                        const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
     if (!ctx) return fail(QH_EINVAL, "gemm: null");
     return gemm_with_scratch(ctx, stream, w, x, ldx, n, out_rows, n_out, y, epi, keys, whole,
-                             Scratch{ctx->argmax_scratch, ctx->sk_scratch});
+                             ctx_scratch(ctx));
 }
 
 extern "C" int qh_gemm_lora(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, void* y,
                             int epi, int whole, const qh_lora* lora) {
     if (!ctx) return fail(QH_EINVAL, "gemm lora: null");
     return gemm_with_scratch(ctx, stream, w, x, ldx, n, nullptr, 0, y, epi, nullptr, whole,
-                             Scratch{ctx->argmax_scratch, ctx->sk_scratch}, lora);
+                             ctx_scratch(ctx), lora);
 }
 
 extern "C" int qh_put_block(qh_ctx* ctx, void* stream, qh_mat* m, const qh_quant* q, const uint8_t* zeros,

@@ -53,14 +53,19 @@ struct Launch {
     int ks, whole, dry_run;
     // an unmerged LoRA adapter's delta fused into the epilogue (lora_rank 0: none): plain products add it to split 0,
     // SwiGLU products to gate and up before the activation (kernels.hip lora_delta16 / lora_delta32)
-    const float* lora_xa;        // the stacked A product's partials [lora_split][m][lora_cols]
+    const float* lora_xa;        // the stacked A product's partials [lora_split][lora_ldm][lora_cols]
     int lora_split, lora_cols, lora_rank;
+    int lora_ldm;                // token rows between xa's partials (m, or the whole step's when run in token chunks)
     int skinny;                  // the skinny kernel takes the product (else the prefill kernel)
     int lora_stage;              // prefill: the item's xa rows staged in LDS (one split, 4 to 32 columns, aligned)
     const uint16_t* lora_b;      // B f16 [rows][lora_rank], the product's row order
     const int* lora_tab;         // module end rows (3 used), then each module's first column of xa (-1: none)
     const int* lora_tok_slot;
     const float* lora_slot_scale;
+    // f16 copies of the activations for prefill launches with f16 operands (kernels.hip prefill_h16): x16_bytes of
+    // scratch; longer steps run in token chunks that fit it
+    void* x16;
+    size_t x16_bytes;
     uint32_t bf16_magic;    // 0x43004300: the bf16 pair (128, 128) (see kernels.hip i4_biased)
     uint32_t nib_mask;      // 0x000F000F
     hipStream_t stream;
@@ -113,9 +118,12 @@ enum { EPI_PLAIN = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
 struct Scratch {
     void* argmax;
     void* stream_k;
+    void* x16;  // X16_SCRATCH_BYTES: f16 activations of prefill launches with f16 operands
 };
 constexpr size_t ARGMAX_SCRATCH_BYTES = (size_t)ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8 + 256;
 constexpr size_t PF_SK_SCRATCH_BYTES = PF_SK_PART_BYTES + PF_SK_ITEMS_MAX * sizeof(unsigned);
+// f16 activations of a prefill launch with f16 operands: 3276 tokens of K = 5120 (the 27B [gate; up] product) at once
+constexpr size_t X16_SCRATCH_BYTES = (size_t)32 << 20;
 
 // The kernels of one storage format F and epilogue EPI: the skinny kernel for m <= SKINNY_MAX_M, else the prefill
 // kernel.

@@ -38,6 +38,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // Kernel format F: bit flags of the storage (kernels.h F_*).
 
@@ -70,26 +72,35 @@ __device__ __forceinline__ bf16x8 i8_biased(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
-// int4 word -> bf16 of (q - z) s = q s + off, in f32 then rounded once
+// two f32 -> the 16-bit pair of the prefill operands: bf16 (v_cvt_pk_bf16_f32) or, H16, f16 (v_cvt_pk_f16_f32), both
+// nearest even
+template <bool H16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    const f32x2 f = {a, b};
+    if constexpr (H16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// int4 word -> 16-bit (bf16, or f16 with H16) of (q - z) s = q s + off, in f32 then rounded once
+template <bool H16 = false>
 __device__ __forceinline__ bf16x8 i4_scaled(uint32_t w, float s, float off) {
     uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
     // opaque to the optimizer: otherwise it folds the nibble mask into each byte extraction and loses the one-op
     // byte-to-float conversions (v_cvt_f32_ubyte0..3)
     asm("" : "+v"(lo));
     asm("" : "+v"(hi));
-    // each bf16 pair is one two-wide conversion (v_cvt_pk_bf16_f32), so no halves are spliced afterwards
+    // each pair is one two-wide conversion (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32), so no halves are spliced afterwards
     auto pair = [&](uint32_t v, int b0, int b1) {
-        const f32x2 f = {__builtin_fmaf(byte_f(v, b0), s, off), __builtin_fmaf(byte_f(v, b1), s, off)};
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+        return pack2<H16>(__builtin_fmaf(byte_f(v, b0), s, off), __builtin_fmaf(byte_f(v, b1), s, off));
     };
     const u32x4 r = {pair(lo, 0, 2), pair(hi, 0, 2), pair(lo, 1, 3), pair(hi, 1, 3)};
     return __builtin_bit_cast(bf16x8, r);
 }
 
+template <bool H16 = false>
 __device__ __forceinline__ bf16x8 i8_scaled(uint32_t a, uint32_t b, float s, float off) {
-    auto pair = [&](uint32_t v, int b0) {  // one v_cvt_pk_bf16_f32 per pair, as i4_scaled
-        const f32x2 f = {__builtin_fmaf(byte_f(v, b0), s, off), __builtin_fmaf(byte_f(v, b0 + 1), s, off)};
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    auto pair = [&](uint32_t v, int b0) {  // one two-wide conversion per pair, as i4_scaled
+        return pack2<H16>(__builtin_fmaf(byte_f(v, b0), s, off), __builtin_fmaf(byte_f(v, b0 + 1), s, off));
     };
     const u32x4 r = {pair(a, 0), pair(a, 2), pair(b, 0), pair(b, 2)};
     return __builtin_bit_cast(bf16x8, r);
@@ -207,7 +218,7 @@ __device__ __forceinline__ void lora_xs_run(const Launch& a, int tok, int c, flo
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = 0.0f;
     for (int sp = 0; sp < a.lora_split; sp++) {
-        const float* p = a.lora_xa + ((size_t)sp * a.m + tok) * a.lora_cols + c;
+        const float* p = a.lora_xa + ((size_t)sp * a.lora_ldm + tok) * a.lora_cols + c;
 #pragma unroll
         for (int i = 0; i < N; i++) v[i] += p[i];
     }
@@ -698,8 +709,22 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
 // who arrives last; its own share from its registers when it is the item's first segment, the usual case), runs the
 // epilogue and clears the counter. No workgroup ever waits for another.
 
+// H16: the operands are f16 (v_mfma_f32_32x32x16_f16, the same rate), else bf16
+template <bool H16 = false>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, bf16x8 b, f32x16 c) {
+    if constexpr (H16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+}
+
+// Whether a prefill launch runs f16 operands: SwiGLU products of int4 and grouped int8 weights. Their activations come
+// converted to f16 (x16_kernel) and each dequantized weight (q - z) s rounds once to f16, the reference's own operands
+// (f16 activations, weights rounded to f16 in its Marlin dequant): 8 times finer than bf16 rounding, which the
+// epilogue's product of two outputs would otherwise carry beyond the bar. Other products keep bf16: dense bf16 and
+// per-channel int8 weights are exact there, and plain outputs hold the bar with bf16 weights.
+__host__ __device__ constexpr bool prefill_h16(int fmt, int epi) {
+    return epi == EPI_SILU && !(fmt & (F_BF16 | F_PERCH));
 }
 
 constexpr int PF_BK = 64;            // columns per LDS stage (half a group; 128-column stages measured the same)
@@ -732,6 +757,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     constexpr int STAGE = BM * PF_ROW;               // LDS bytes of one stage
     constexpr int NW = WM * WN;                      // waves
     constexpr int NACC = BMB * TN * 16;              // accumulator registers per lane
+    constexpr bool H16 = prefill_h16(F, EPI);        // f16 operands (activations converted by x16_kernel)
     // two objects, so that the compiler can tell the direct-to-LDS loads into one from the reads of the other
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
@@ -839,8 +865,8 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
         const int pc = kk & 1, i = kk >> 1;
         if (F & F_BF16) return __builtin_bit_cast(bf16x8, f.c[t][pc][i]);  // step kk's piece as stored
         if (F & F_I8)  // int8: word pair (2e, 2e + 1) of half h, for k32 step i = 2h + e
-            return i8_scaled(f.c[t][pc][i >> 1][2 * (i & 1)], f.c[t][pc][i >> 1][2 * (i & 1) + 1], sc, off);
-        return i4_scaled(f.c[t][pc][0][i], sc, off);
+            return i8_scaled<H16>(f.c[t][pc][i >> 1][2 * (i & 1)], f.c[t][pc][i >> 1][2 * (i & 1) + 1], sc, off);
+        return i4_scaled<H16>(f.c[t][pc][0][i], sc, off);
     };
 
     f32x16 acc[BMB][TN];
@@ -880,7 +906,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
 #pragma unroll
             for (int bb = 0; bb < BMB; bb++)
 #pragma unroll
-                for (int t = 0; t < TN; t++) acc[bb][t] = mfma32(xa[s16 & 1][bb], bw[t], acc[bb][t]);
+                for (int t = 0; t < TN; t++) acc[bb][t] = mfma32<H16>(xa[s16 & 1][bb], bw[t], acc[bb][t]);
         }
         __builtin_amdgcn_s_setprio(0);
     };
@@ -967,7 +993,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             const u32x4 cur = ring[f % LA];
             if (f + LA < NF) ring[f % LA] = *addr(f + LA);
 #pragma unroll
-            for (int t = 0; t < TN; t++) acc[f % BMB][t] = mfma32(cur, bwg[f / BMB][t], acc[f % BMB][t]);
+            for (int t = 0; t < TN; t++) acc[f % BMB][t] = mfma32<H16>(cur, bwg[f / BMB][t], acc[f % BMB][t]);
         }
         // the order above, kept by the scheduler: LA reads, then each MFMA followed by the next read
         __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
@@ -1385,7 +1411,23 @@ static hipError_t launch_fmt(Launch& l) {
     }
 }
 
-hipError_t launch(Launch& l) {
+// bf16 activations rows [0, m) (ldx elements apart) -> f16 [m][cols], nearest even (v_cvt_pk_f16_f32; beyond f16's
+// range to infinity, as the reference's f16 activations would be): 8 values per thread
+__global__ __launch_bounds__(256) void x16_kernel(const uint16_t* x, int ldx, int m, int cols, uint16_t* out) {
+    const int per_row = cols / 8;
+    const size_t n = (size_t)m * per_row;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / per_row, c = 8 * (i - r * per_row);
+        const u32x4 v = *(const u32x4*)(x + r * ldx + c);
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            o[j] = pack2<true>(__uint_as_float(v[j] << 16), __uint_as_float(v[j] & 0xffff0000u));
+        *(u32x4*)(out + r * cols + c) = o;
+    }
+}
+
+static hipError_t launch_any(Launch& l) {
     switch (l.fmt) {
         case F_I4: return launch_fmt<F_I4>(l);
         case F_I4 | F_S32: return launch_fmt<F_I4 | F_S32>(l);
@@ -1396,6 +1438,36 @@ hipError_t launch(Launch& l) {
         case F_BF16: return launch_fmt<F_BF16>(l);
         default: return hipErrorInvalidValue;
     }
+}
+
+// A prefill launch with f16 operands: the activations converted into the x16 scratch first, in token chunks that fit
+// it (each chunk one conversion and one product launch, on the same stream; the LoRA adapter's rows follow the chunk).
+static hipError_t launch_h16(Launch& l) {
+    const size_t per = l.x16 ? l.x16_bytes / ((size_t)l.cols * 2) : 0;
+    if (per == 0 || l.xrows) return hipErrorInvalidValue;
+    for (int t0 = 0; t0 < l.m; t0 += (int)per) {
+        Launch c = l;
+        c.m = (int)std::min<size_t>(per, (size_t)(l.m - t0));
+        const unsigned blocks = (unsigned)std::min<size_t>(((size_t)c.m * l.cols / 8 + 255) / 256, 2048);
+        hipLaunchKernelGGL(x16_kernel, dim3(blocks), dim3(256), 0, l.stream, (const uint16_t*)l.x + (size_t)t0 * l.ldx,
+                           l.ldx, c.m, l.cols, (uint16_t*)l.x16);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        c.x = l.x16;
+        c.ldx = l.cols;
+        c.y = (uint16_t*)l.y + (size_t)t0 * l.ldy;
+        if (l.lora_rank) {
+            c.lora_xa = l.lora_xa + (size_t)t0 * l.lora_cols;
+            c.lora_tok_slot = l.lora_tok_slot + t0;
+        }
+        if (hipError_t e = launch_any(c); e != hipSuccess) return e;
+        l.split = c.split;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch(Launch& l) {
+    if (!l.skinny && !l.dry_run && prefill_h16(l.fmt, l.epi)) return launch_h16(l);
+    return launch_any(l);
 }
 #endif
 

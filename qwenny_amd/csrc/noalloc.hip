@@ -2,8 +2,9 @@
 // array instead of the context's allocations, for callers that cannot allocate device memory around a product (code
 // under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
 //
-// The array holds, in this order, the argmax table and its workgroup counter (ARGMAX_SCRATCH_BYTES) and the prefill's
-// stream-K partials and item counters (PF_SK_SCRATCH_BYTES): the same scratch qh_open allocates per context, so both
+// The array holds, in this order, the argmax table and its workgroup counter (ARGMAX_SCRATCH_BYTES), the prefill's
+// stream-K partials and item counters (PF_SK_SCRATCH_BYTES) and the f16 activations of prefill launches with f16
+// operands (X16_SCRATCH_BYTES): the same scratch qh_open allocates per context, so both
 // entry points make the same launch plans and the same results. Every GPU the library runs on holds its own copy
 // until the process ends. In host code `scratch` names a host-side stand-in, not device memory: its device address on
 // each GPU is resolved once per device by noalloc_init (called by qh_open with the device current) and only that
@@ -13,6 +14,7 @@
 // GPU (two streams, two threads, two contexts on the same device) share the array and race.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "gemm.h"
@@ -22,18 +24,21 @@ namespace qh {
 
 constexpr size_t NOALLOC_ARGMAX_OFF = 0;
 constexpr size_t NOALLOC_SK_OFF = (ARGMAX_SCRATCH_BYTES + 255) & ~(size_t)255;
-constexpr size_t NOALLOC_BYTES = NOALLOC_SK_OFF + PF_SK_SCRATCH_BYTES;  // 128 MiB + 48.25 KiB
+constexpr size_t NOALLOC_X16_OFF = NOALLOC_SK_OFF + PF_SK_SCRATCH_BYTES;
+constexpr size_t NOALLOC_BYTES = NOALLOC_X16_OFF + X16_SCRATCH_BYTES;  // 160 MiB + 48.25 KiB
 
 static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 
 constexpr int MAX_DEVICES = 64;
-static void* scratch_ptr[MAX_DEVICES];  // device address of `scratch` on each device, null until set up
+// device address of `scratch` on each device, null until set up: stored (release) under scratch_mu once the array is
+// cleared, read (acquire) without the lock by every call
+static std::atomic<void*> scratch_ptr[MAX_DEVICES];
 static std::mutex scratch_mu;
 
 int noalloc_init(int device) {
     if (device < 0 || device >= MAX_DEVICES) return fail(QH_EINVAL, "no-alloc scratch: device %d", device);
     std::lock_guard<std::mutex> g(scratch_mu);
-    if (scratch_ptr[device]) return QH_OK;
+    if (scratch_ptr[device].load(std::memory_order_acquire)) return QH_OK;
     void* ptr = nullptr;
     hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !ptr)
@@ -45,7 +50,7 @@ int noalloc_init(int device) {
         e = hipMemset((uint8_t*)ptr + NOALLOC_SK_OFF + PF_SK_PART_BYTES, 0, PF_SK_SCRATCH_BYTES - PF_SK_PART_BYTES);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return fail(QH_EHIP, "no-alloc scratch on device %d: clear: %s", device, hipGetErrorString(e));
-    scratch_ptr[device] = ptr;
+    scratch_ptr[device].store(ptr, std::memory_order_release);
     return QH_OK;
 }
 
@@ -57,8 +62,9 @@ extern "C" int qh_gemm_noalloc(qh_ctx* ctx, void* stream, const qh_mat* w, const
                                const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole) {
     if (!ctx) return fail(QH_EINVAL, "gemm (no-alloc): null");
     const int device = ctx_device(ctx);
-    void* ptr = device >= 0 && device < MAX_DEVICES ? scratch_ptr[device] : nullptr;
+    void* ptr = device >= 0 && device < MAX_DEVICES ? scratch_ptr[device].load(std::memory_order_acquire) : nullptr;
     if (!ptr) return fail(QH_EINVAL, "gemm (no-alloc): scratch of device %d not set up (qh_open)", device);
     return gemm_with_scratch(ctx, stream, w, x, ldx, n, out_rows, n_out, y, epi, keys, whole,
-                             Scratch{(uint8_t*)ptr + NOALLOC_ARGMAX_OFF, (uint8_t*)ptr + NOALLOC_SK_OFF});
+                             Scratch{(uint8_t*)ptr + NOALLOC_ARGMAX_OFF, (uint8_t*)ptr + NOALLOC_SK_OFF,
+                                     (uint8_t*)ptr + NOALLOC_X16_OFF});
 }

@@ -62,6 +62,25 @@ def emulate_bf16_weights(q, x):
     return bf16_to_f32(x).astype(np.float64) @ w.astype(np.float64).T
 
 
+def emulate_f16_operands(q, x):
+    """What the prefill kernel computes by design for SwiGLU products of int4 and grouped int8 weights (f16 operands,
+    the reference's own): each weight (q - z) s rounded once to f16, the activations converted to f16 (nearest even),
+    products and sums exact (f64 here)."""
+    from qwenny_amd.synth import bf16_to_f32
+
+    w = dequant_f32(q).astype(np.float16).astype(np.float64)
+    xh = bf16_to_f32(x).astype(np.float16).astype(np.float64)
+    return xh @ w.T
+
+
+def emulate_silu_prefill(q, x):
+    """The gate or up product as the prefill kernel's SwiGLU launches compute it (f16 operands, but per-channel int8
+    exact as in every prefill product)."""
+    if q.bits == 8 and q.group == q.cols:
+        return emulate_bf16_weights(q, x)
+    return emulate_f16_operands(q, x)
+
+
 def bf16_out_err(got, want):
     """max over outputs of (|got - want| - one bf16 ulp of want) / RMS(want): the error beyond the rounding of a
     bf16 output."""
@@ -78,3 +97,20 @@ def rel_err(got, want):
     want = np.asarray(want, np.float64)
     rms = np.sqrt(np.mean(want * want))
     return float(np.max(np.abs(got - want)) / max(rms, 1e-30))
+
+
+def silu_bar(got, g, u, tol=TOL):
+    """The product bar carried through the SwiGLU epilogue. g and u: the exact gate and up products (f64 [m][rows/2],
+    the oracle's); each is allowed max |err| <= tol * RMS, i.e. |dg| <= dg_max = tol RMS(g), |du| <= du_max =
+    tol RMS(u), and silu'(v) lies in [-0.0999, 1.0999], so an output computed from products within the bar lies within
+    |silu(g)| du_max + 1.1 dg_max (|u| + du_max) of silu(g) u, plus the bf16 rounding of the output (one ulp).
+    Returns max over outputs of (|got - silu(g) u| - ulp) / that bound: at most 1 for outputs within the bar."""
+    got = np.asarray(got, np.float64)
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    sg = g / (1.0 + np.exp(-g))
+    want = sg * u
+    dg, du = tol * np.sqrt(np.mean(g * g)), tol * np.sqrt(np.mean(u * u))
+    bound = np.abs(sg) * du + 1.1 * dg * (np.abs(u) + du)
+    ulp = np.abs(want) * 2.0 ** -8
+    return float(np.max(np.maximum(np.abs(got - want) - ulp, 0.0) / bound))

@@ -13,8 +13,8 @@ import pytest
 import oracle
 from qwenny_amd import SKINNY_MAX_M, Epi, Mat, Wt, row_order
 from qwenny_amd.synth import activations, bf16_to_f32
-from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, sub_quant,
-                           to_dev)
+from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, emulate_silu_prefill, make_quant, oracle_y, rel_err,
+                           silu_bar, sub_quant, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -91,10 +91,15 @@ def test_silu(gemm, kind, m):
         full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1)
         tol = TOL
     else:
-        full = np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
+        full = np.concatenate([emulate_silu_prefill(gate, x), emulate_silu_prefill(up, x)], axis=1)
         tol = 1e-3
     want = oracle.silu_glu(full, row_order(n, True))
     assert bf16_out_err(got, want) <= tol
+    # every kernel also against the oracle's exact dequantize-then-matmul: at the product bar carried through the
+    # epilogue, and within the bar of the output itself
+    g, u = oracle_y(gate, x), oracle_y(up, x)
+    assert silu_bar(got, g, u) <= 1.0
+    assert bf16_out_err(got, oracle.silu_glu(np.concatenate([g, u], axis=1), None)) <= TOL
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -189,9 +194,13 @@ def test_kernel_switch_large_int4(gemm):
         if gu.kernel(m, Epi.Silu) == "skinny":
             g, u, tol = oracle_y(sg, x), oracle_y(su, x), TOL
         else:
-            g, u, tol = emulate_bf16_weights(sg, x), emulate_bf16_weights(su, x), 1e-3
+            g, u, tol = emulate_silu_prefill(sg, x), emulate_silu_prefill(su, x), 1e-3
         want = oracle.silu_glu(np.concatenate([g, u], axis=1), None)
         assert bf16_out_err(y.float().cpu().numpy()[:, half], want) <= tol
+        # both kernels against the oracle's exact product at the bar
+        eg, eu = oracle_y(sg, x), oracle_y(su, x)
+        assert silu_bar(y.float().cpu().numpy()[:, half], eg, eu) <= 1.0
+        assert bf16_out_err(y.float().cpu().numpy()[:, half], oracle.silu_glu(np.concatenate([eg, eu], 1), None)) <= TOL
     for m in (32, 33, 48):
         print(f"kernel switch m={m}", flush=True)
         x = activations(183 + m, "x", m, k, outliers=0.01)

@@ -18,7 +18,8 @@ import oracle
 from qwenny_amd import SKINNY_MAX_M, Epi, Mat, Wt
 from qwenny_amd.core import Quant
 from qwenny_amd.synth import activations, f32_to_bf16
-from tests.helpers import TOL, bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, sub_quant, to_dev
+from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, emulate_silu_prefill, make_quant, oracle_y, rel_err,
+                           silu_bar, sub_quant, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -121,12 +122,16 @@ def test_grouped_int8_silu(gemm, way, m):
         g, u = oracle_y(sg, x), oracle_y(su, x)
         tol = TOL
     else:
-        g, u = emulate_bf16_weights(sg, x), emulate_bf16_weights(su, x)
-        # the epilogue's inputs carry each weight's bf16 rounding (the gate and up products themselves are held to
-        # the north star's bar against the oracle by test_grouped_int8_plain); the epilogue is checked against silu
-        # over that arithmetic
+        g, u = emulate_silu_prefill(sg, x), emulate_silu_prefill(su, x)
+        # the epilogue's inputs carry each weight's f16 rounding and the activations' conversion to f16; the epilogue
+        # is checked against silu over that arithmetic
         tol = 1e-3
     assert bf16_out_err(got, g / (1.0 + np.exp(-g)) * u) <= tol
+    # both kernels against the oracle's exact product: the product bar carried through the epilogue, and the bar of
+    # the output itself
+    eg, eu = oracle_y(sg, x), oracle_y(su, x)
+    assert silu_bar(got, eg, eu) <= 1.0
+    assert bf16_out_err(got, eg / (1.0 + np.exp(-eg)) * eu) <= TOL
 
 
 @pytest.mark.parametrize("way", ["checkpoint", "requant"])

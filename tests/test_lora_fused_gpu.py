@@ -4,7 +4,8 @@ the unfused path (the product, then the lora_add / lora_silu consumers, kernels/
 Plain products: the partials' sum must be W x + s_t B (A x) — the kernel's own product arithmetic (exact at decode
 sizes, bf16-rounded weights above 48 tokens) plus the oracle's f64 delta, to 1e-4 of RMS — and the delta lands on
 split 0 only (the other partials equal the plain product's). SwiGLU products: silu(gate + dg) (up + du) against the
-oracle's lora_silu over the kernel's product, to one bf16 ulp plus 1e-3 of RMS. Cases cover both kernels and every
+oracle's lora_silu over the kernel's product (exact at decode sizes, f16 operands above 48 tokens), to one bf16 ulp
+plus 1e-3 of RMS. Cases cover both kernels and every
 prefill plan (K slices, stream-K, whole items), every rank, xa of 1-3 split-K partials, module ends inside tiles,
 an unadapted module, and tokens of slot scale 0.
 """
@@ -15,7 +16,7 @@ import pytest
 import oracle
 from qwenny_amd import SKINNY_MAX_M, Epi, Mat, row_order
 from qwenny_amd.synth import activations
-from tests.helpers import bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, to_dev
+from tests.helpers import bf16_out_err, emulate_bf16_weights, emulate_silu_prefill, make_quant, oracle_y, rel_err, to_dev
 
 pytestmark = pytest.mark.gpu
 INT_MAX = 2**31 - 1
@@ -100,7 +101,7 @@ def test_lora_silu_fused(gemm, m, rank, split, half, k):
     got = mid.float().cpu().numpy()
     order = row_order(rows, True)
     full = np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1) if mat.kernel(m, Epi.Silu) == "skinny" else \
-        np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
+        np.concatenate([emulate_silu_prefill(gate, x), emulate_silu_prefill(up, x)], axis=1)
     packed = full[:, order]  # the product in its packed (SwiGLU) row order
     xa, b, tab_h, tok_slot, slot_scale = host
     want = oracle.lora_silu(packed, xa, split, b, rank, tab_h, tok_slot, slot_scale, m)

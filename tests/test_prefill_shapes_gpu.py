@@ -11,8 +11,8 @@ import pytest
 import oracle
 from qwenny_amd import Epi, Mat, row_order
 from qwenny_amd.synth import activations
-from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, make_quant, oracle_y, rel_err, sub_quant,
-                           to_dev)
+from tests.helpers import (TOL, bf16_out_err, emulate_bf16_weights, emulate_silu_prefill, make_quant, oracle_y, rel_err,
+                           silu_bar, sub_quant, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -53,9 +53,12 @@ def test_shape_256x192_silu(gemm):
     assert gemm.run(None, m, mat, to_dev(x), y, Epi.Silu) == 1
     torch.cuda.synchronize()
     got = y.float().cpu().numpy()
-    full = np.concatenate([emulate_bf16_weights(gate, x), emulate_bf16_weights(up, x)], axis=1)
+    full = np.concatenate([emulate_silu_prefill(gate, x), emulate_silu_prefill(up, x)], axis=1)
     want = oracle.silu_glu(full, row_order(n, True))
     assert bf16_out_err(got, want) <= 1e-3
+    g, u = oracle_y(gate, x), oracle_y(up, x)
+    assert silu_bar(got, g, u) <= 1.0
+    assert bf16_out_err(got, oracle.silu_glu(np.concatenate([g, u], axis=1), None)) <= TOL
 
 
 def test_shape_256x192_dense_bf16(gemm):

@@ -44,3 +44,31 @@ def test_tuned_partition_matches_default(gemm, monkeypatch, env, m):
         assert rel_err(got_sum, oracle_y(q, x)) <= 1e-4
     finally:
         tuned.close()
+
+
+@pytest.mark.parametrize("pk", ["2", "4"])
+def test_part_len_covers_tuned_split(monkeypatch, pk):
+    """Under QH_SKINNY_PLAIN_WK the skinny split depends on the token count; part_len must cover the largest
+    split x tokens over every count (a product into a part_len-sized buffer writes no further)."""
+    import torch
+
+    print(f"part_len QH_SKINNY_PLAIN_WK={pk}", flush=True)
+    monkeypatch.setenv("QH_SKINNY_PLAIN_WK", pk)
+    tuned = Gemm.load(0)
+    try:
+        q = make_quant(950, "i4", 1024, 4096)
+        mat = Mat.stack(tuned, [q])
+        max_tok = 48
+        need = max(mat.split(m) * m * mat.rows for m in range(1, max_tok + 1))
+        n = tuned.part_len([mat], max_tok)
+        assert n >= need
+        # a product of every token count into a buffer of exactly part_len floats, guarded by a canary after it
+        y = torch.full((n + 4096,), float("nan"), dtype=torch.float32, device="cuda")
+        for m in (1, 2, 3, 4, 16, 17, 33, 48):
+            x = activations(951 + m, "x", m, 4096)
+            split = tuned.run(None, m, mat, to_dev(x), y, Epi.Plain)
+            assert split * m * mat.rows <= n
+        torch.cuda.synchronize()
+        assert torch.isnan(y[n:]).all()
+    finally:
+        tuned.close()

@@ -107,3 +107,35 @@ def test_noalloc_rejects_too_many_argmax_rows(gemm):
     with pytest.raises(QhError) as e:
         _call(lib().qh_gemm_noalloc, gemm, mat, x, 65, y, Epi.Argmax, keys, 65)
     assert "at most 64" in str(e.value)
+
+
+def test_noalloc_allocates_nothing(gemm):
+    """The property the entry point exists for: a run of calls (decode split-K, stream-K prefill, argmax) leaves the
+    device's free memory unchanged (hipMemGetInfo), after one warm-up call per kernel (the runtime loads code objects
+    on a kernel's first launch)."""
+    import torch
+
+    print("no-alloc memory check", flush=True)
+    cases = []
+    for kind, n, k, m, epi in (("i4", 6144, 5120, 1, Epi.Plain), ("i4", 4096, 4096, 256, Epi.Plain),
+                               ("i4", 65536, 512, 5, Epi.Argmax)):
+        mat = Mat.stack(gemm, [make_quant(940 + m, kind, n, k)])
+        x = to_dev(activations(941 + m, "x", m, k))
+        rows = m
+        split = mat.split(m) if epi == Epi.Plain else 1
+        y = torch.zeros((split, rows, mat.rows), dtype=torch.float32, device="cuda")
+        keys = torch.zeros(m, dtype=torch.int64, device="cuda") if epi == Epi.Argmax else None
+        cases.append((mat, x, m, y, epi, keys, m if epi == Epi.Argmax else 0, 1 if m == 256 else 0))
+
+    def run_all():
+        for mat, x, m, y, epi, keys, n_out, whole in cases:
+            _call(lib().qh_gemm_noalloc, gemm, mat, x, m, y, epi, keys, n_out, whole)
+
+    run_all()
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(5):
+        run_all()
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
