@@ -449,7 +449,7 @@ def consumers_line(args):
     tab_add = torch.tensor([2**31 - 1] * 4 + [0, -1, -1, -1], dtype=torch.int32, device="cuda")
     tab_silu = torch.tensor([2**31 - 1] * 4 + [0, rank, -1, -1], dtype=torch.int32, device="cuda")
     scale = torch.tensor([1.0], dtype=torch.float32, device="cuda")
-    for m, split in ((1, 34), (2048, 1)):
+    for m, split in ((1, 34), (1, 1), (2048, 1)):
         x = torch.randn(split, m, hid, device="cuda", generator=g)
         h = torch.randn(m, hid, device="cuda", generator=g)
         w = torch.ones(hid, device="cuda")
@@ -469,6 +469,8 @@ def consumers_line(args):
                           m * mcols * 4 + gu * rank * 2 * -(-m // 16) + m * gu * 4 + m * gu),
         }
         for name, (fn, nbytes) in cases.items():
+            if split == 1 and m == 1 and name not in ("add_rmsnorm", "sum_parts"):
+                continue  # one partial at M = 1: the residual step's cost without the split-K partials
             for _ in range(3):
                 fn()
             torch.cuda.synchronize()
@@ -489,9 +491,71 @@ def consumers_line(args):
             t1.record()
             torch.cuda.synchronize()
             s = t0.elapsed_time(t1) / (reps * 20) * 1e-3
-            out[f"{name}_m{m}"] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 1)}
-            print(f"# {name} M={m}: {s * 1e6:.2f} us, {nbytes / s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+            key = f"{name}_m{m}" + ("_split1" if m == 1 and split == 1 else "")
+            out[key] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 1)}
+            print(f"# {key}: {s * 1e6:.2f} us, {nbytes / s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
     return {"consumers": out}
+
+
+class LayerStep:
+    """One 27B decode layer's quantized products at M = 1 as the engine runs them, each with the consumer of its
+    output (4 device copies): the attention in-projection (5120 -> 6144, plain) then the sum of its partials (standing
+    in for attn_prep, which reads the same partials); the out-projection (6144 -> 5120) and the down projection
+    (17408 -> 5120), plain, each then the residual step (add_rmsnorm over its partials); [gate; up] (5120 -> 2 x 17408)
+    with the SwiGLU epilogue (whole sums, no partials)."""
+
+    def __init__(self, gemm, set_mats, gate_up):
+        import torch
+
+        self.gemm = gemm
+        self.x = torch.randn(1, 17408, device="cuda").to(torch.bfloat16)
+        self.h = torch.randn(1, 5120, device="cuda")
+        self.w = torch.ones(5120, device="cuda")
+        self.yb = torch.empty(1, 5120, dtype=torch.bfloat16, device="cuda")
+        self.mid = torch.empty(1, 17408, dtype=torch.bfloat16, device="cuda")
+        self.ys = torch.empty(1, 6144, device="cuda")
+        self.parts = {}
+        self.launches = []
+        for c in range(4):
+            for mat, kind in ((set_mats[3][c], "in"), (set_mats[4][c], "res"), (gate_up[c], "silu"),
+                              (set_mats[2][c], "res")):
+                split = mat.split(1) if kind != "silu" else 1
+                if (mat.rows, split) not in self.parts:
+                    self.parts[(mat.rows, split)] = torch.empty(split, 1, mat.rows, device="cuda")
+                self.launches.append((mat, kind, self.parts[(mat.rows, split)]))
+
+    def run(self, stream=None):
+        from qwenny_amd import Epi, add_rmsnorm, sum_parts
+
+        for mat, kind, y in self.launches:
+            if kind == "silu":
+                self.gemm.run(stream, 1, mat, self.x, self.mid, Epi.Silu)
+                continue
+            split = self.gemm.run(stream, 1, mat, self.x, y, Epi.Plain)
+            if kind == "in":
+                sum_parts(stream, y, split, 1, mat.rows, self.ys)
+            else:
+                add_rmsnorm(stream, self.h, y, split, 1, 5120, self.w, self.yb)
+
+    def bytes(self):
+        k, n = 5120, 2 * 17408  # [gate; up]: int4 codes and scales, x once, bf16 output of n / 2 rows
+        gate_up = k * n // 2 + (k // 128) * n * 2 + 2 * k + (n // 2) * 2
+        return 4 * (int4_bytes(5120, 6144, 1) + int4_bytes(6144, 5120, 1) + gate_up + int4_bytes(17408, 5120, 1))
+
+
+def layer_line(gemm, set_mats, args):
+    """The decode layer as the engine runs it (LayerStep): HBM GB/s over the products' algorithmic bytes, beside the
+    products alone (the same products, no consumers)."""
+    from qwenny_amd import Mat
+
+    gate, up = quant(100, "i4", 5120, 17408), quant(101, "i4", 5120, 17408)
+    gate_up = [Mat.stack(gemm, [gate, up], silu=True) for _ in range(4)]
+    st = LayerStep(gemm, set_mats, gate_up)
+    ms = time_step(st, args.steps, args.warmup, not args.no_graph)
+    out = {"ms_per_step": round(ms, 5), "GBps": round(st.bytes() / (ms * 1e-3) / 1e9, 1)}
+    print(f"# decode layer x4 as the engine runs it (products + consumers): {ms:.4f} ms, {out['GBps']} GB/s",
+          file=sys.stderr, flush=True)
+    return {"m1_layer_with_consumers": out}
 
 
 class SummedStep(Step):
@@ -722,7 +786,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of lines: m1,m1sum,m5,prefill,pfzp,pfshort,int8,i8g,dense,dequant,set4b,c0,consumers,"
-                         "lora")
+                         "lora,layer")
     ap.add_argument("--traffic-run", action="store_true", help="the rocprofv3 --pmc workload (see traffic_run)")
     ap.add_argument("--with-torch", action="store_true",
                     help="--prefill-run: also run each shape as a dense bf16 torch product (hipBLASLt)")
@@ -766,7 +830,7 @@ def main():
         print(json.dumps({"set4b_run": "done"}))
         return
     only = set(args.only.split(",")) if args.only else {"m1", "m1sum", "m5", "prefill", "pfzp", "pfshort", "int8", "i8g", "dense",
-                                                         "dequant", "set4b", "c0", "consumers", "lora"}
+                                                         "dequant", "set4b", "c0", "consumers", "lora", "layer"}
     print("# generating the 27B-scale layer set and head", file=sys.stderr, flush=True)
     set_mats = [upload_copies(gemm, quant(100 + i, "i4", k, n), 4) for i, (k, n) in enumerate(SET_27B)]
     if args.traffic_run:
@@ -905,6 +969,8 @@ def main():
         extra.update(grouped_int8_line(gemm, args))
     if "pfzp" in only:
         extra.update(prefill_zp_line(gemm, args))
+    if "layer" in only:
+        extra.update(layer_line(gemm, set_mats, args))
 
     line = {
         "metric": "int4 GEMM HBM GB/s (% of 8 TB/s) at M=1/5; TFLOP/s (% bf16 MFMA peak) at M=2048",
