@@ -5,7 +5,9 @@ bf16 does not hold exactly, so the loader stores them as QH_WT_I4_S32 (f32 scale
 are served here (the reference's group-64 cases and its int8 case, with zero point 8 rather than 128, do not fit the
 tile layout); output rows are padded to whole 16-row tiles with zero-weight rows. Every case is a decode-sized
 product (1-8 tokens) on the skinny kernel, whose products are exact, so the reference test's own bar applies:
-|got - want| < 2e-5 (1 + |want|) (src/mlx/metal.rs:404-406)."""
+|got - want| < 2e-5 (1 + |want|) (src/mlx/metal.rs:404-406). The same generator at the 27B-scale shapes of the
+reference's packed-layout test (src/mlx/metal.rs:430-485: [gate; up] 34816 x 5120, down 5120 x 17408, the 248,320-row
+head, at 5 and 8 tokens) is held to that test's bar, max |got - want| < 2e-4."""
 
 import os
 
@@ -61,3 +63,37 @@ def test_mlx_affine_golden(gemm, i, whole):
     assert (got[:, n:] == 0).all()
     err = np.abs(got[:, :n] - want)
     assert (err < 2e-5 * (1 + np.abs(want))).all(), err.max()
+
+
+# the 27B-scale shapes of the reference's packed-layout test (src/mlx/metal.rs:436-444; (m, n, k), group 128):
+# inputs from the same closed-form generator, expected products in f64 from the stored values, the test's own bar:
+# max |got - want| < 2e-4 (src/mlx/metal.rs:478-480)
+SHAPES_27B = [(5, 256, 1024), (8, 384, 5120), (5, 34816, 5120), (5, 5120, 17408), (5, 248320, 5120)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES_27B)
+def test_mlx_affine_27b_shapes(gemm, m, n, k):
+    import torch
+
+    from tests.golden.make_golden import mlx_case
+    from tests.test_full_output_gpu import _Dequant
+    from qwenny_amd.synth import bf16_to_f32, f32_to_bf16
+
+    print(f"golden generator 27B shape m={m} n={n} k={k}", flush=True)
+    x16, q, sc, bi = mlx_case(m, n, k, 128, 4)
+    quant = Quant(4, 128, n, k, q, sc.astype(np.float32).reshape(-1), bi.astype(np.float32).reshape(-1))
+    mat = Mat.stack(gemm, [quant])
+    assert mat.wt == Wt.I4_S32 and mat.kernel(m) == "skinny"
+    xb = f32_to_bf16(x16.astype(np.float32))
+    split = mat.split(m)
+    y = torch.full((split, m, n), float("nan"), dtype=torch.float32, device="cuda")
+    assert gemm.run(None, m, mat, to_dev(xb), y, Epi.Plain) == split
+    torch.cuda.synchronize()
+    got = y.double().sum(0).cpu().numpy()
+    xf = bf16_to_f32(xb).astype(np.float64)
+    dq = _Dequant(quant, 4096)
+    worst = 0.0
+    for r0 in range(0, n, 4096):
+        r1 = min(n, r0 + 4096)
+        worst = max(worst, float(np.abs(got[:, r0:r1] - xf @ dq.rows(r0, r1).T).max()))
+    assert worst < 2e-4, worst
