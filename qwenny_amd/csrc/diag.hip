@@ -23,20 +23,21 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void diag_read_kernel(const u32x4* p, int tiles, int groups, int pattern,
                                                         uint32_t never, uint32_t* sink) {
     const int lane = threadIdx.x & 63, wt = threadIdx.x >> 6;
-    const u32x4* b[8];
+    // block offsets (in 16-byte units) of the wave's 8 blocks; loads straight off `p`, so that they stay global loads
+    size_t o[8];
     if (pattern == 0) {
         const size_t w = (size_t)blockIdx.x * (blockDim.x >> 6) + wt;
 #pragma unroll
-        for (int i = 0; i < 8; i++) b[i] = p + (w * 8 + i) * 64 + lane;
+        for (int i = 0; i < 8; i++) o[i] = (w * 8 + i) * 64 + lane;
     } else {
         const int t0 = 2 * (blockIdx.x * (blockDim.x >> 6) + wt), g0 = 4 * blockIdx.y;
         if (t0 >= tiles) return;
 #pragma unroll
-        for (int i = 0; i < 8; i++) b[i] = p + ((size_t)(t0 + (i & 1)) * groups + g0 + (i >> 1)) * 64 + lane;
+        for (int i = 0; i < 8; i++) o[i] = ((size_t)(t0 + (i & 1)) * groups + g0 + (i >> 1)) * 64 + lane;
     }
     u32x4 v[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = __builtin_nontemporal_load(b[i]);
+    for (int i = 0; i < 8; i++) v[i] = __builtin_nontemporal_load(p + o[i]);
     uint32_t s = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) s ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
