@@ -375,17 +375,19 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
     const int l16 = lane & 15, kq = lane >> 4;
     const int tiles = a.rows / TILE, G = a.cols / QG, M = a.m;
     const int CH = WK * NG, NC = a.nc;  // groups per super-chunk, super-chunks in K
-    // super-chunks [c0, c1) of this split: one each (plain products), all (split 1), else an even share
-    int c0, c1;
-    if (a.split == NC) {
-        c0 = blockIdx.y;
-        c1 = c0 + 1;
-    } else if (a.split == 1) {
-        c0 = 0;
-        c1 = NC;
-    } else {
-        c0 = (int)(blockIdx.y * (unsigned)NC / (unsigned)a.split);
-        c1 = (int)((blockIdx.y + 1) * (unsigned)NC / (unsigned)a.split);
+    // super-chunks [c0, c1) of this split: one each (split-K plain products: split == NC), else all (split 1; the
+    // launcher makes no other split), chosen without a branch so that no scalar load waits ahead of the next
+    const bool per_chunk = a.split == NC;
+    const int c0 = per_chunk ? (int)blockIdx.y : 0, c1 = per_chunk ? c0 + 1 : NC;
+    // activation rows are gathered (out_rows) only by the argmax epilogue
+    const int32_t* const xrows = EPI == EPI_ARGMAX ? a.xrows : nullptr;
+    // the loop's operands loaded here with the fields above, in one batch of scalar loads and one wait, rather than
+    // a second round trip in the loop's preheader
+    {
+        const void* const ops[4] = {a.codes, a.scales, a.x, (F & F_ZP) ? (const void*)a.zeros : a.y};
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm volatile("" ::"s"(ops[i]));
+        asm volatile("" ::"s"(a.ldx));
     }
     const int tile0 = (blockIdx.x * WT + wt) * T;
     const int xpitch = CH * QG + 8;  // bf16 per staged x row (+16 bytes: rows start 4 banks apart)
@@ -431,9 +433,9 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
         const int p = tid + i * nthr;
         const int tok = min(p / rowc, M - 1), pc = p - (p / rowc) * rowc;
         xo[i] = p < npieces ? tok * xpitch + 8 * pc : -1;
-        xsrc[i] = (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + 8 * (p < npieces ? pc : 0);
+        xsrc[i] = (const __bf16*)a.x + (size_t)(xrows ? xrows[tok] : tok) * a.ldx + 8 * (p < npieces ? pc : 0);
     }
-    const __bf16* xwsrc = (const __bf16*)a.x + (size_t)(PRIV && a.xrows ? a.xrows[0] : 0) * a.ldx + 8 * lane;
+    const __bf16* xwsrc = (const __bf16*)a.x + (size_t)(PRIV && xrows ? xrows[0] : 0) * a.ldx + 8 * lane;
 
     for (int c = c0; c < c1; c++) {
         const int gs = c * CH;              // first group of the super-chunk
@@ -494,7 +496,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
             for (int p = tid + XPT * nthr; p < npieces; p += nthr) {
                 const int tok = p / rowc, pc = p - tok * rowc;
                 const __bf16* src =
-                    (const __bf16*)a.x + (size_t)(a.xrows ? a.xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
+                    (const __bf16*)a.x + (size_t)(xrows ? xrows[tok] : tok) * a.ldx + (size_t)gs * QG + 8 * pc;
                 *(u32x4*)(xs_lds + (size_t)tok * xpitch + 8 * pc) = *(const u32x4*)src;
             }
             __syncthreads();
@@ -1298,6 +1300,7 @@ static hipError_t skinny_ng(const Launch& l) {
     Launch k = l;
     const int wk = l.waves / l.tile_waves;
     k.nc = l.cols / QG / (wk * NG);
+    if (l.split != 1 && l.split != k.nc) return hipErrorInvalidConfiguration;  // the kernel's two cases
     hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.tile_waves, wk),
                        skinny_lds(l), l.stream, k);
     return hipGetLastError();
