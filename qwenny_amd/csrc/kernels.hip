@@ -565,7 +565,8 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
 #pragma unroll
                 for (int b = 0; b < TB; b++)
 #pragma unroll
-                    for (int r = 0; r < NR; r++) acc[b][t][r] += sc * (d[b][r] - cz * xsum[b][r]);
+                    for (int r = 0; r < NR; r++)  // two explicit fmas (the one-token kernel's too: equal results)
+                        acc[b][t][r] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[b][r], d[b][r]), acc[b][t][r]);
             }
         }
     }
@@ -682,58 +683,71 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// skinny_m1_kernel: the one-token plain product of symmetric int4 (bf16 scales) with no adapter, the decode hot path,
-// as skinny_kernel runs it (the same partition, loads, arithmetic and partials, so the same results bit for bit)
-// with a compact argument block and no paths for other cases. skinny_kernel reads a 300-byte Launch whose fields its
-// index set-up and branches need one after another (each scalar load round trip ahead of the wave's first global
-// load); here every argument comes with the first scalar loads. Same-box graph replays, per launch: (5120, 17408)
-// and (17408, 5120) 10.1-10.3 -> 9.7 us, (5120, 6144) 5.55 -> 5.1 us in a standalone copy of this kernel.
+// skinny_m1_kernel: the one-token plain product of int4 with bf16 scales, symmetric or with zero points (ZP), with
+// no adapter, the decode hot path, as skinny_kernel runs it (the same partition, loads, arithmetic and partials, so the
+// same results bit for bit) with a compact argument block and no paths for other cases. skinny_kernel reads a
+// 300-byte Launch and carries every other case's set-up ahead of its first global load. Same-box graph replays, per
+// launch: the 27B set 8.15 -> 7.40 us (symmetric; (5120, 17408) and (17408, 5120) 10.1-10.3 -> 9.7 us, (5120, 6144)
+// 5.55 -> 5.1 us), configs[0] 4.93 -> 4.49 us.
 struct M1Args {
     const u32x4* codes;
     const uint16_t* scales;
+    const uint16_t* zeros;  // ZP only
     const __bf16* x;
-    float* y;  // [G / 4][tiles * 16]: the partial of each 4-group chunk of K
+    float* y;  // [G / NG][tiles * 16]: the partial of each NG-group chunk of K
     int tiles, G;
     uint32_t mask, magic;  // 0x000F000F and the bf16 pair (128, 128): see i4_biased
 };
 
-// workgroups of 4 waves side by side over tiles (2 tiles each), the grid over tile columns x 4-group chunks of K
+// workgroups of 4 waves side by side over tiles (2 tiles each), the grid over tile columns x NG-group chunks of K
+// (NG = 4, or 1 when 4-group waves would not fill the chip; skinny_partition)
+template <bool ZP, int NG>
 static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63, wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, kq = lane >> 4;
     const int T = a.tiles, G = a.G;
-    const int tile0 = (blockIdx.x * 4 + wt) * 2, gw = 4 * blockIdx.y;
+    const int tile0 = (blockIdx.x * 4 + wt) * 2, gw = NG * blockIdx.y;
     if (tile0 >= T) return;
     const int t1 = min(tile0 + 1, T - 1);  // an odd last tile: its wave reads the same tile twice, stores once
     __bf16* xw = (__bf16*)smem + wt * 4 * QG;
     uint32_t magic;  // in a VGPR, so that each pair is one v_and_or_b32
     asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
     const uint32_t mask = a.mask;
-    // the wave's 4 groups of activations, global -> LDS directly, first: its own slot, no workgroup barrier
-    __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)gw * QG + 8 * lane), (__attribute__((address_space(3))) void*)xw,
-                                     16, 0, 0);
+    // the wave's groups of activations, global -> LDS directly, first, into its own slot (no workgroup barrier);
+    // one group (NG = 1): each quarter of the wave loads the same 256 bytes, read from the first copy
+    const int xl = NG == 4 ? lane : l16;
+    __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)gw * QG + 8 * xl),
+                                     (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    // scales (4 groups per 8-byte load), then the codes group by group, streamed past the caches
-    uint32_t sraw[2][2];
+    // scales (4 groups per 8-byte load, or the one group's), zero points, then the codes group by group, streamed
+    // past the caches
+    constexpr int SW = NG == 4 ? 2 : 1;
+    uint32_t sraw[2][SW], zraw[2];
     const int tl[2] = {tile0, t1};
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-        const unsigned long long v =
-            __builtin_nontemporal_load((const unsigned long long*)(a.scales + scale_idx(tl[t], T, gw, l16)));
-        sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
+        const uint16_t* sp = a.scales + scale_idx(tl[t], T, gw, l16);
+        if constexpr (NG == 4) {
+            const unsigned long long v = __builtin_nontemporal_load((const unsigned long long*)sp);
+            sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
+        } else {
+            sraw[t][0] = __builtin_nontemporal_load(sp);
+        }
+        if (ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tl[t], T, gw, l16));
     }
-    u32x4 code[4][2];
+    u32x4 code[NG][2];
 #pragma unroll
-    for (int gi = 0; gi < 4; gi++)
+    for (int gi = 0; gi < NG; gi++)
 #pragma unroll
         for (int t = 0; t < 2; t++) code[gi][t] = __builtin_nontemporal_load(a.codes + ((size_t)tl[t] * G + gw + gi) * 64 + lane);
-    // the activations landed (the 10 weight loads issued after them may stay in flight)
-    __builtin_amdgcn_s_waitcnt((10 & 15) | (7 << 4) | (15 << 8));
+    // the activations landed (the weight loads issued after them may stay in flight)
+    constexpr int WL = 2 + (ZP ? 2 : 0) + 2 * NG;
+    __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
     const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
     float acc[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (int gi = 0; gi < 4; gi++) {
+    for (int gi = 0; gi < NG; gi++) {
         u32x4 xa[4];
         const __bf16* xrow = xw + gi * QG + 8 * kq;
 #pragma unroll
@@ -746,9 +760,15 @@ static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
             f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < 4; j++) d = mfma(xa[j], i4_biased(code[gi][t][j], mask, magic), d);
-            const uint32_t w = sraw[t][gi >> 1];
-            const float sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
-            acc[t] += sc * (d[0] - 136.0f * xsum[0]);
+            float sc;
+            if constexpr (NG == 4) {
+                const uint32_t w = sraw[t][gi >> 1];
+                sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
+            } else {
+                sc = __uint_as_float(sraw[t][0] << 16);
+            }
+            const float cz = ZP ? (float)(128 + (int)((zraw[t] >> (4 * ((gw + gi) & 3))) & 15u)) : 136.0f;
+            acc[t] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[0], d[0]), acc[t]);  // as skinny_kernel
         }
     }
     if (kq == 0) {
@@ -1317,16 +1337,21 @@ static hipError_t skinny_nr(const Launch& l) {
 // token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
-    if constexpr (F == F_I4 && EPI == EPI_PLAIN) {
+    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
         // the lean one-token kernel: the partition skinny_partition gives a plain one-token product (4 wave columns of
-        // 2 tiles, one 4-group chunk of K per wave, split = G / 4), no adapter, activations in their own rows
-        const int G = l.cols / QG;
-        if (l.m == 1 && !l.lora_rank && !l.xrows && l.groups_per_wave == 4 && l.tile_waves == 4 && l.waves == 4 &&
-            l.split == G / 4 && !l.stage_out) {
+        // 2 tiles, one chunk of 4 groups, or of one, of K per wave, split = the chunks), no adapter, activations in
+        // their own rows
+        const int G = l.cols / QG, ng = l.groups_per_wave;
+        if (l.m == 1 && !l.lora_rank && !l.xrows && (ng == 4 || ng == 1) && l.tile_waves == 4 && l.waves == 4 &&
+            l.split == G / ng && !l.stage_out) {
             const int tiles = l.rows / TILE;
-            const M1Args a{(const u32x4*)l.codes, (const uint16_t*)l.scales, (const __bf16*)l.x, (float*)l.y,
-                           tiles, G, l.nib_mask, l.bf16_magic};
-            hipLaunchKernelGGL(skinny_m1_kernel, dim3((tiles + 7) / 8, G / 4), dim3(256), 4 * 4 * QG * 2, l.stream, a);
+            const M1Args a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x,
+                           (float*)l.y, tiles, G, l.nib_mask, l.bf16_magic};
+            const dim3 grid((tiles + 7) / 8, G / ng);
+            if (ng == 4)
+                hipLaunchKernelGGL((skinny_m1_kernel<F == F_ZP, 4>), grid, dim3(256), 4 * 4 * QG * 2, l.stream, a);
+            else
+                hipLaunchKernelGGL((skinny_m1_kernel<F == F_ZP, 1>), grid, dim3(256), 4 * 4 * QG * 2, l.stream, a);
             return hipGetLastError();
         }
     }
