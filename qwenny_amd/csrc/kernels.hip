@@ -778,6 +778,125 @@ static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
     }
 }
 
+// skinny_mt_kernel: the plain product of 2-5 tokens (up to 8 fit the slots) on the same terms as skinny_m1_kernel (int4 with bf16 scales,
+// symmetric or with zero points, no adapter): the partition of skinny_kernel's plain products (WT wave columns of 2
+// tiles per workgroup, one chunk of NG groups of K per wave, split = the chunks) and its arithmetic (one MFMA row
+// block of 16 tokens, token 4 (lane / 16) + r in row r of a lane's accumulators), bit for bit. Each wave stages its
+// own tokens' activations (M rows of NG groups, rows 16 bytes apart, global -> LDS directly), so no workgroup barrier
+// separates its loads from its compute, and writes its partials through its LDS slot as 16-byte row runs.
+struct MtArgs {
+    const u32x4* codes;
+    const uint16_t* scales;
+    const uint16_t* zeros;  // ZP only
+    const __bf16* x;
+    int ldx;
+    float* y;  // [G / NG][m][tiles * 16]
+    int tiles, G, m;
+    uint32_t mask, magic;
+};
+
+template <int NG>
+__host__ __device__ constexpr int mt_xpitch() { return NG * QG + 8; }  // bf16 per staged row (16 bytes of padding)
+
+template <bool ZP, int NG, int NR>
+static __global__ __launch_bounds__(512) void skinny_mt_kernel(MtArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int XP = mt_xpitch<NG>();
+    const int lane = threadIdx.x & 63, wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int WT = blockDim.x >> 6;
+    const int l16 = lane & 15, kq = lane >> 4;
+    const int T = a.tiles, G = a.G, M = a.m;
+    const int tile0 = (blockIdx.x * WT + wt) * 2, gw = NG * blockIdx.y;
+    if (tile0 >= T) return;
+    const int t1 = min(tile0 + 1, T - 1);
+    __bf16* xw = (__bf16*)smem + (size_t)wt * M * XP;  // the wave's slot: its M rows (and then its partials)
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
+    const uint32_t mask = a.mask;
+    // the activations first: row r into slot row r (NG = 4: 64 lanes x 16 bytes; NG = 1: 16 lanes)
+    for (int r = 0; r < M; r++) {
+        if (NG == 4 || lane < 16)
+            __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)r * a.ldx + (size_t)gw * QG + 8 * lane),
+                                             (__attribute__((address_space(3))) void*)(xw + r * XP), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int SW = NG == 4 ? 2 : 1;
+    uint32_t sraw[2][SW], zraw[2];
+    const int tl[2] = {tile0, t1};
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const uint16_t* sp = a.scales + scale_idx(tl[t], T, gw, l16);
+        if constexpr (NG == 4) {
+            const unsigned long long v = __builtin_nontemporal_load((const unsigned long long*)sp);
+            sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
+        } else {
+            sraw[t][0] = __builtin_nontemporal_load(sp);
+        }
+        if (ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tl[t], T, gw, l16));
+    }
+    u32x4 code[NG][2];
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) code[gi][t] = __builtin_nontemporal_load(a.codes + ((size_t)tl[t] * G + gw + gi) * 64 + lane);
+    // the activations landed (the weight loads issued after them may stay in flight)
+    constexpr int WL = 2 + (ZP ? 2 : 0) + 2 * NG;
+    __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    float acc[2][NR];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) acc[t][r] = 0.0f;
+    const __bf16* xrow0 = xw + min(l16, M - 1) * XP + 8 * kq;  // rows past M read row M - 1 (never stored)
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+        u32x4 xa[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow0 + gi * QG + 32 * j);
+        f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            bf16x8 bw[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) bw[j] = i4_biased(code[gi][t][j], mask, magic);
+            f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) d = mfma(xa[j], bw[j], d);
+            float sc;
+            if constexpr (NG == 4) {
+                const uint32_t w = sraw[t][gi >> 1];
+                sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
+            } else {
+                sc = __uint_as_float(sraw[t][0] << 16);
+            }
+            const float cz = ZP ? (float)(128 + (int)((zraw[t] >> (4 * ((gw + gi) & 3))) & 15u)) : 136.0f;
+#pragma unroll
+            for (int r = 0; r < NR; r++) acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[r], d[r]), acc[t][r]);
+        }
+    }
+    // the partials through the wave's own slot (its activation reads are done: LDS reads complete in order, and the
+    // compiler waits for each before its MFMA): M tokens x 32 rows, then 16-byte stores of 128-byte row runs
+    float* stg = (float*)xw;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const int tok = 4 * kq + r;
+            if (tok < M) stg[tok * 32 + t * TILE + l16] = acc[t][r];
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes before its reads
+    const int rows = a.tiles * TILE, nrow = min(32, rows - tile0 * TILE);
+    float* yb = a.y + (size_t)blockIdx.y * M * rows + tile0 * TILE;
+    for (int i = lane; i < M * 8; i += 64) {
+        const int tok = i >> 3, c = 4 * (i & 7);
+        if (c < nrow)
+            __builtin_nontemporal_store(*(const f32x4*)(stg + tok * 32 + c), (f32x4*)(yb + (size_t)tok * rows + c));
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // prefill_kernel
 //
@@ -1352,6 +1471,36 @@ static hipError_t skinny_epi(const Launch& l) {
                 hipLaunchKernelGGL((skinny_m1_kernel<F == F_ZP, 4>), grid, dim3(256), 4 * 4 * QG * 2, l.stream, a);
             else
                 hipLaunchKernelGGL((skinny_m1_kernel<F == F_ZP, 1>), grid, dim3(256), 4 * 4 * QG * 2, l.stream, a);
+            return hipGetLastError();
+        }
+        // the lean kernel for 2-5 tokens, on the same partition. Same-box graph replays: the 27B step at M = 5
+        // 0.302 -> 0.282 ms, the 4B set with zero points at M = 2 4.28 -> 3.95 us per launch, at M = 4 and 5 level;
+        // at M = 8 it lost 3% (its per-wave staging grows the workgroup's LDS with the token count), so from 6 tokens
+        // skinny_kernel's shared staging
+        const int wt = l.tile_waves;
+        if (l.m >= 2 && l.m <= 5 && !l.lora_rank && !l.xrows && (ng == 4 || ng == 1) && l.waves == wt &&
+            wt <= 8 && l.split == G / ng && ((uintptr_t)l.y & 15) == 0) {
+            const int tiles = l.rows / TILE;
+            const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
+                           (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
+            const dim3 grid((tiles + 2 * wt - 1) / (2 * wt), G / ng), block(64 * wt);
+            // per wave: m staged rows, which also hold its m x 32 partials (m x 128 bytes) afterwards
+            const size_t lds = (size_t)wt * l.m * (ng == 4 ? mt_xpitch<4>() : mt_xpitch<1>()) * 2;
+            auto go = [&](auto NGc, auto NRc) {
+                hipLaunchKernelGGL((skinny_mt_kernel<F == F_ZP, decltype(NGc)::value, decltype(NRc)::value>), grid,
+                                   block, lds, l.stream, a);
+            };
+            using I1 = std::integral_constant<int, 1>;
+            using I4 = std::integral_constant<int, 4>;
+            if (ng == 4) {
+                if (l.m == 2) go(I4{}, std::integral_constant<int, 2>{});
+                else if (l.m == 3) go(I4{}, std::integral_constant<int, 3>{});
+                else go(I4{}, I4{});
+            } else {
+                if (l.m == 2) go(I1{}, std::integral_constant<int, 2>{});
+                else if (l.m == 3) go(I1{}, std::integral_constant<int, 3>{});
+                else go(I1{}, I4{});
+            }
             return hipGetLastError();
         }
     }
