@@ -236,7 +236,7 @@ def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
                 name = r["Kernel_Name"]
                 kind = "diag" if "diag_read_kernel" in name else (
                     "copy" if ("copy" in name.lower() and "skinny" not in name) else (
-                        "skinny" if "skinny_kernel" in name else None))
+                        "skinny" if ("skinny_kernel" in name or "skinny_m1_kernel" in name) else None))
                 if kind:
                     out.setdefault(kind, []).append(float(r["Counter_Value"]))
         return out
@@ -250,7 +250,7 @@ def summarize_traffic(fetch_dir, write_dir, out_name=TRAFFIC_NAME):
     fdiag = max(fetch["diag"]) if fetch.get("diag") else None
     ffac = COPY_BYTES / (fdiag * 1024) if fdiag else cfac
     fk, wk = mean(fetch["skinny"]) * 1024 * ffac, mean(write["skinny"]) * 1024 * wfac
-    res = {"kernel": "skinny_kernel int4 M=1, 27B layer set (5 shapes x 4 copies)",
+    res = {"kernel": "skinny_m1_kernel (int4 plain M=1), 27B layer set (5 shapes x 4 copies)",
            "fetch_kib_per_dispatch": mean(fetch["skinny"]), "write_kib_per_dispatch": mean(write["skinny"]),
            "copy_fetch_kib": fcopy, "copy_write_kib": wcopy, "copy_bytes": COPY_BYTES,
            "diag_read_fetch_kib": fdiag, "copy_fetch_scale": cfac,
@@ -992,7 +992,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(per_launch_bytes / per_launch_s / 1e9, 1), "peak": HBM_PEAK,
                      "unit": "GB/s", "frac": round(per_launch_bytes / per_launch_s / 1e9 / HBM_PEAK, 4),
                      "traffic": load_traffic(TRAFFIC_NAME),
-                     "kernel": "skinny_kernel<int4, plain, M=1> over the 27B set (20 launches)",
+                     "kernel": "skinny_m1_kernel<int4 symmetric, 4 groups per wave> (plain M=1) over the 27B set (20 launches)",
                      "bytes_per_launch": round(per_launch_bytes), "us_per_launch": round(per_launch_s * 1e6, 3)},
         "extra": extra,
     }
