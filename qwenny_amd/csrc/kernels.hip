@@ -138,35 +138,39 @@ __device__ __forceinline__ unsigned long long group16_max(unsigned long long k) 
 // this part, far too costly once per workgroup. Every table and counter update is a returning device-scope atomic
 // (performed at the device's coherence point); a workgroup waits for its own to return before it counts itself done,
 // and the last workgroup reads the table with atomic exchanges after its count returned.
-__device__ __forceinline__ void argmax_spread_max(const Launch& a, int tok, unsigned long long k) {
+__device__ __forceinline__ void argmax_spread_max(unsigned long long* table, int tok, unsigned long long k) {
     const int row = (blockIdx.y * gridDim.x + blockIdx.x) % ARGMAX_SPREAD;
-    (void)__hip_atomic_fetch_max(a.argmax_table + row * ARGMAX_MAX_TOK + tok, k, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+    (void)__hip_atomic_fetch_max(table + row * ARGMAX_MAX_TOK + tok, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void argmax_spread_max(const Launch& a, int tok, unsigned long long k) {
+    argmax_spread_max(a.argmax_table, tok, k);
 }
 
-__device__ void argmax_finish(const Launch& a, int tid, int nthr) {
+__device__ void argmax_finish(unsigned long long* table, unsigned* count, unsigned long long* keys, int m, int tid,
+                              int nthr) {
     __shared__ int last;
     __shared__ unsigned long long best[ARGMAX_MAX_TOK];
     __builtin_amdgcn_s_waitcnt(0);  // this wave's table updates have returned
     __syncthreads();
     if (tid == 0)
-        last = __hip_atomic_fetch_add(a.argmax_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                gridDim.x * gridDim.y - 1;
-    for (int t = tid; t < a.m; t += nthr) best[t] = 0;
+    for (int t = tid; t < m; t += nthr) best[t] = 0;
     __syncthreads();
     if (!last) return;  // uniform over the workgroup
-    for (int i = tid; i < ARGMAX_SPREAD * a.m; i += nthr) {
-        const int row = i / a.m, tok = i - row * a.m;
-        const unsigned long long k = __hip_atomic_exchange(a.argmax_table + row * ARGMAX_MAX_TOK + tok, 0ull,
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = tid; i < ARGMAX_SPREAD * m; i += nthr) {
+        const int row = i / m, tok = i - row * m;
+        const unsigned long long k =
+            __hip_atomic_exchange(table + row * ARGMAX_MAX_TOK + tok, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (k) atomicMax(best + tok, k);
     }
     __syncthreads();
-    for (int t = tid; t < a.m; t += nthr)
-        if (best[t])
-            (void)__hip_atomic_fetch_max(a.keys + t, best[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid == 0)
-        (void)__hip_atomic_exchange(a.argmax_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int t = tid; t < m; t += nthr)
+        if (best[t]) (void)__hip_atomic_fetch_max(keys + t, best[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) (void)__hip_atomic_exchange(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ void argmax_finish(const Launch& a, int tid, int nthr) {
+    argmax_finish(a.argmax_table, a.argmax_count, a.keys, a.m, tid, nthr);
 }
 
 // Words of a (tile, group) code block per lane (16 bytes each).
@@ -776,6 +780,108 @@ static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
         yo[0] = acc[0];
         if (tile0 + 1 < T) yo[TILE] = acc[1];
     }
+}
+
+// skinny_m1w_kernel: one-token products that need whole sums (the SwiGLU epilogue; argmax too, not dispatched) of
+// int4 with bf16
+// scales, symmetric or with zero points, no adapter, on the lean terms of skinny_m1_kernel: a workgroup takes one
+// pair of tiles over all of K, one wave per 4-group chunk (WK = G / 4 <= 16 waves), each as short-lived as a plain
+// product's; the chunks' sums meet in LDS and the first wave adds them in chunk order. (skinny_kernel runs these with
+// 2 x 2-wave workgroups whose waves each walk G / 8 chunks, one after another.)
+struct M1wArgs {
+    const u32x4* codes;
+    const uint16_t* scales;
+    const uint16_t* zeros;  // ZP only
+    const __bf16* x;
+    void* y;                // SwiGLU: bf16 [rows / 2]; argmax: f32 logits [rows]
+    unsigned long long* keys;
+    unsigned long long* table;  // the argmax spread table and its workgroup counter (argmax_finish)
+    unsigned* count;
+    int tiles, G, valid;
+    uint32_t mask, magic;
+};
+
+template <int EPI, bool ZP>
+static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int WK = blockDim.x >> 6;
+    const int l16 = lane & 15, kq = lane >> 4;
+    const int T = a.tiles, G = a.G;
+    const int tile0 = blockIdx.x * 2, gw = 4 * wk;
+    const int t1 = min(tile0 + 1, T - 1);
+    __bf16* xw = (__bf16*)smem + wk * 4 * QG;
+    float* red = (float*)(smem + (size_t)WK * 4 * QG * 2);  // [WK][32]: each chunk's sums of the 32 rows
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
+    const uint32_t mask = a.mask;
+    __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)gw * QG + 8 * lane),
+                                     (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t sraw[2][2], zraw[2];
+    const int tl[2] = {tile0, t1};
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const unsigned long long v =
+            __builtin_nontemporal_load((const unsigned long long*)(a.scales + scale_idx(tl[t], T, gw, l16)));
+        sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
+        if (ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tl[t], T, gw, l16));
+    }
+    u32x4 code[4][2];
+#pragma unroll
+    for (int gi = 0; gi < 4; gi++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) code[gi][t] = __builtin_nontemporal_load(a.codes + ((size_t)tl[t] * G + gw + gi) * 64 + lane);
+    constexpr int WL = 2 + (ZP ? 2 : 0) + 8;
+    __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int gi = 0; gi < 4; gi++) {
+        u32x4 xa[4];
+        const __bf16* xrow = xw + gi * QG + 8 * kq;
+#pragma unroll
+        for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow + 32 * j);
+        f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) d = mfma(xa[j], i4_biased(code[gi][t][j], mask, magic), d);
+            const uint32_t w = sraw[t][gi >> 1];
+            const float sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
+            const float cz = ZP ? (float)(128 + (int)((zraw[t] >> (4 * gi)) & 15u)) : 136.0f;
+            acc[t] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[0], d[0]), acc[t]);
+        }
+    }
+    if (kq == 0) {
+        red[wk * 32 + l16] = acc[0];
+        red[wk * 32 + TILE + l16] = acc[1];
+    }
+    __syncthreads();
+    if (wk == 0) {
+        // row tile0 * 16 + lane of the pair (lanes 0..31): the chunks in K order
+        float v = 0.0f;
+        for (int c = 0; c < WK; c++) v += red[c * 32 + (lane & 31)];
+        const int tile = tile0 + (lane >> 4 & 1), out = tile * TILE + l16;
+        const bool ok = lane < 32 && tile < T;
+        if (EPI == EPI_SILU) {
+            const float up = __shfl_xor(v, 8);  // rows 8..15 of a tile are the up rows of rows 0..7
+            if (ok && l16 < 8) ((__bf16*)a.y)[tile * 8 + l16] = (__bf16)(silu(v) * up);
+        } else {
+            unsigned long long k = 0;
+            if (ok) {
+                ((float*)a.y)[out] = v;
+                if (out < a.valid) k = argmax_key(v, out);
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) k = max_u64(k, __shfl_xor(k, o));
+            if (lane == 0 && k) argmax_spread_max(a.table, 0, k);
+        }
+    }
+    if (EPI == EPI_ARGMAX) argmax_finish(a.table, a.count, a.keys, 1, threadIdx.x, blockDim.x);
 }
 
 // skinny_mt_kernel: the plain product of 2-5 tokens (up to 8 fit the slots) on the same terms as skinny_m1_kernel (int4 with bf16 scales,
@@ -1456,6 +1562,22 @@ static hipError_t skinny_nr(const Launch& l) {
 // token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
+    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_SILU) {
+        // one token, SwiGLU: the lean workgroup-per-tile-pair kernel when K has at most 16 chunks of 4 groups.
+        // Same-box graph replays, the 27B [gate; up] product (2 x 17408 rows, K 5120): 20.6 -> 18.9 us. The argmax
+        // epilogue stays on skinny_kernel: on the 27B head the twice as many workgroups, each counting itself done
+        // with a returning atomic, made it 20% slower (106 -> 128 us).
+        const int G = l.cols / QG;
+        if (l.m == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && G / 4 <= 16) {
+            const int tiles = l.rows / TILE, wk = G / 4;
+            const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
+                            l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
+            const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
+            hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
+                               a);
+            return hipGetLastError();
+        }
+    }
     if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
         // the lean one-token kernel: the partition skinny_partition gives a plain one-token product (4 wave columns of
         // 2 tiles, one chunk of 4 groups, or of one, of K per wave, split = the chunks), no adapter, activations in
