@@ -141,8 +141,9 @@ int qh_unpack_row_bf16(size_t rows, size_t cols, const void* codes, size_t p, ui
 /* ---- device: context, matrices, products ---------------------------------------------------------------------- */
 
 /* Gemm::load (core.rs:436-481): a context on `device` (makes it current on this thread). It holds the argmax scratch
- * table and the prefill's stream-K scratch (128 MiB of partial tiles and 4096 item counters), both returned to zero by
- * every launch; products on one context must therefore not run concurrently on two streams. */
+ * table and counter, the prefill's stream-K scratch (128 MiB of partial tiles and 4096 item counters) and 32 MiB
+ * for the f16 activations of the prefill's SwiGLU launches, all returned to zero by every launch that uses them;
+ * products on one context must therefore not run concurrently on two streams. */
 int qh_open(int device, qh_ctx** out);
 void qh_close(qh_ctx* ctx);
 
@@ -230,11 +231,13 @@ int qh_gemm_lora(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size
 
 /* qh_gemm without allocation: no counterpart in the reference. For callers that cannot allocate device memory around
  * a product (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments,
- * checks, launch plans and results as qh_gemm, but the launch scratch (argmax table, stream-K partials and counters)
- * lives in a static device array of the library (128 MiB + 48.25 KiB per GPU, held until the process ends, set up by
- * qh_open) instead of the context's allocations; it calls no allocating routine. Products never need more scratch
- * than that (the launch planner sizes stream-K to it; argmax takes at most 64 logit rows, QH_EINVAL beyond). Calls
- * that overlap on one GPU share the array and race: serialise them (one stream). */
+ * checks, launch plans and results as qh_gemm, but the launch scratch (argmax table and counter, stream-K partials
+ * and counters, the f16 activations of prefill SwiGLU launches) lives in a static device array of the library
+ * (160 MiB + 48.25 KiB per GPU, held until the process ends, set up by qh_open; every process that loads the library
+ * reserves it) instead of the context's allocations; it calls no allocating routine. Products never need more scratch
+ * than that (the launch planner sizes stream-K to it; longer SwiGLU steps run in token chunks; argmax takes at most 64
+ * logit rows, QH_EINVAL beyond). Calls that overlap on one GPU share the array and race: serialise them (one
+ * stream). */
 int qh_gemm_noalloc(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
                     const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole);
 
