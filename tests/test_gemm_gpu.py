@@ -57,6 +57,39 @@ def test_skinny_plain(gemm, kind, m):
     _check(_plain(gemm, mat, x, m), q, x, mat.kernel(m))
 
 
+@pytest.mark.parametrize("kind", ["i4", "i4z"])
+@pytest.mark.parametrize("m", [1, 2, 5])
+@pytest.mark.parametrize("rows,cols", [(16, 512), (48, 512), (80, 1024), (400, 2560)])
+def test_decode_odd_tiles(gemm, kind, m, rows, cols):
+    """Decode products of 1, 3, 5 and 25 tiles (the last wave of a pair holding one tile), with 4-group and one-group
+    waves: the lean decode kernels' edges. Each output against the oracle; the returned split matches Mat.split."""
+    print(f"decode odd tiles {kind} m={m} {rows}x{cols}", flush=True)
+    q = make_quant(60 + rows + m, kind, rows, cols)
+    x = activations(61 + m, "x", m, cols)
+    mat = Mat.stack(gemm, [q])
+    got = _plain(gemm, mat, x, m)
+    assert rel_err(got, oracle_y(q, x)) <= 1e-4
+
+
+@pytest.mark.parametrize("kind", ["i4", "i4z"])
+@pytest.mark.parametrize("half,cols", [(24, 512), (40, 2560), (8, 6144)])
+def test_silu_decode_odd_tiles(gemm, kind, half, cols):
+    """One-token SwiGLU over 3, 5 and 1 tiles of [gate; up], K of 4, 20 and 48 groups (the lean one-token SwiGLU
+    kernel takes K of at most 16 chunks of 4 groups; 48 groups go to skinny_kernel): against the oracle."""
+    import torch
+
+    print(f"silu decode odd tiles {kind} half={half} cols={cols}", flush=True)
+    gate, up = make_quant(70 + half, kind, half, cols), make_quant(71 + half, kind, half, cols)
+    x = activations(72, "x", 1, cols)
+    mat = Mat.stack(gemm, [gate, up], silu=True)
+    y = torch.full((1, half), float("nan"), dtype=torch.bfloat16, device="cuda")
+    assert gemm.run(None, 1, mat, to_dev(x), y, Epi.Silu) == 1
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    want = oracle.silu_glu(np.concatenate([oracle_y(gate, x), oracle_y(up, x)], axis=1), None)
+    assert bf16_out_err(got, want) <= 1e-4
+
+
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("m", [17, 33, 48, 49, 64, 130, 256, 300])
 def test_prefill_plain(gemm, kind, m):
