@@ -1062,6 +1062,22 @@ __device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// 16 bytes per lane global -> LDS (global_load_lds_dwordx4: wave-uniform base + 32-bit lane offset) into the 1 KiB at
+// dst. In inline assembly: the compiler counts its own form of this load against the LDS counter as well and makes the
+// wave's next LDS read wait for the global load to complete (a whole memory round trip before the ping-pong's MFMA
+// phase); the hardware's LDS reads are ordered by the workgroup barriers that already follow every stage's loads.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, lds_ptr dst) {
+    // both wave-uniform by construction; read from the first lane so that they are in scalar registers whatever the
+    // compiler could prove
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    // (readfirstlane returns a signed int: each half is zero-extended before it is put in place)
+    const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(bs), "s"(d)
+                 : "memory", "m0");
+}
+
 // buffer resource word 3 (gfx9: 32-bit data format, no swizzle) and the sc1 cache-policy bit of buffer operations
 constexpr int BUF_RSRC_WORD3 = 0x00020000;
 constexpr int CPOL_SC1 = 16;
@@ -1238,15 +1254,20 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     // acc = the current item's product over groups [g0, g1). The activations go global -> LDS directly
     // (global_load_lds_dwordx4): stage 2g (the group's first 64 columns) is computed from lds0 while stage 2g + 1 loads
     // into lds1 and the next group's weights into registers, then stage 2g + 1 from lds1 while stage 2g + 2 loads into
-    // lds0; each stage ends with one workgroup barrier, whose fence also waits for this wave's loads in flight (the next
-    // stage's activations and the next group's weights: a barrier without the fence, leaving the weights in flight,
-    // measured the same here and slower in the ping-pong schedule).
+    // lds0; each stage ends with a wait for this wave's loads in flight (the next stage's activations and the next
+    // group's weights) and one workgroup barrier.
     auto stage_issue = [&](int st, uint8_t* buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
-            if (NB % NW == 0 || i * NW + wave < NB)  // wave-uniform
-            __builtin_amdgcn_global_load_lds((const void*)(xbase + (size_t)st * PF_ROW + xd[i]),
-                                             (lds_ptr)(buf + (i * NW + wave) * 1024), 16, 0, 0);
+            if (NB % NW == 0 || i * NW + wave < NB) {  // wave-uniform
+                // the ping-pong schedule issues them in inline assembly (measured +3% at 2048 tokens); the shared one
+                // in the compiler's form (1-3% faster there at 256 tokens)
+                if constexpr (PP)
+                    lds_dma16((const void*)(xbase + (size_t)st * PF_ROW), xd[i], (lds_ptr)(buf + (i * NW + wave) * 1024));
+                else
+                    __builtin_amdgcn_global_load_lds((const void*)(xbase + (size_t)st * PF_ROW + xd[i]),
+                                                     (lds_ptr)(buf + (i * NW + wave) * 1024), 16, 0, 0);
+            }
     };
     // LoRA: the item's xa rows (tokens tok0 .., clamped to m - 1) go global -> LDS while the item runs; the run's
     // barriers make them the workgroup's before the epilogue reads them
@@ -1277,6 +1298,7 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
             __builtin_amdgcn_sched_barrier(0);  // the weight loads behind the activation loads
             wload(more ? g + 1 : g, wnxt);
             compute(0, 0, wcur);
+            __builtin_amdgcn_s_waitcnt(0);  // stage 2g + 1, read after the barrier, has landed (and the weights)
             __syncthreads();
             if (more) stage_issue(2 * g + 2, lds0);
             compute(1, 1, wcur);
@@ -1287,8 +1309,9 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     };
     // Ping-pong (PP: 256 x 256 items on 8 waves). The SIMD's two waves (w and w + 4) take turns: while one runs a
     // group's 64 MFMAs (raised issue priority, A fragments read six ahead through a register ring), the other
-    // dequantizes its weights for its next group into registers; a workgroup barrier ends each half. Activations: a group's two stages in one pair of LDS buffers while the next group's load into the
-    // other pair. Against the shared schedule above, same box, M = 2048: int4 (5120, 17408) / (17408, 5120) +2-3%,
+    // dequantizes its weights for its next group into registers; a workgroup barrier ends each half. Activations: a
+    // group's two stages in one pair of LDS buffers while the next group's load into the other pair (issued at the
+    // group's start, waited for only at its end: the barrier between the halves carries no wait for them). Against the shared schedule above, same box, M = 2048: int4 (5120, 17408) / (17408, 5120) +2-3%,
     // int8 +1-3.5%, zero points +3-5%, the fused LoRA delta 0 to +5% (MFMA busy 0.540 -> 0.564 and 0.564 -> 0.599, at a
     // slightly lower clock).
     bf16x8 bwg[2 * PF_K16][TN];  // a group's B fragments, dequantized a half ahead of their MFMAs
