@@ -499,10 +499,11 @@ def consumers_line(args):
 
 class LayerStep:
     """One 27B decode layer's quantized products at M = 1 as the engine runs them, each with the consumer of its
-    output (4 device copies): the attention in-projection (5120 -> 6144, plain) then the sum of its partials (standing
-    in for attn_prep, which reads the same partials); the out-projection (6144 -> 5120) and the down projection
-    (17408 -> 5120), plain, each then the residual step (add_rmsnorm over its partials); [gate; up] (5120 -> 2 x 17408)
-    with the SwiGLU epilogue (whole sums, no partials)."""
+    output (4 device copies): the attention in-projection (5120 -> 6144) as whole rows (one partial, for attn_prep;
+    measured faster than its split product followed by the sum of the partials); the out-projection (6144 -> 5120)
+    and the down projection (17408 -> 5120), plain, each then the residual step (add_rmsnorm over its partials, which
+    reads many partials for little more than one: faster than a whole-row product there); [gate; up] (5120 -> 2 x
+    17408) with the SwiGLU epilogue (whole sums, no partials)."""
 
     def __init__(self, gemm, set_mats, gate_up):
         import torch
@@ -513,29 +514,28 @@ class LayerStep:
         self.w = torch.ones(5120, device="cuda")
         self.yb = torch.empty(1, 5120, dtype=torch.bfloat16, device="cuda")
         self.mid = torch.empty(1, 17408, dtype=torch.bfloat16, device="cuda")
-        self.ys = torch.empty(1, 6144, device="cuda")
         self.parts = {}
         self.launches = []
         for c in range(4):
             for mat, kind in ((set_mats[3][c], "in"), (set_mats[4][c], "res"), (gate_up[c], "silu"),
                               (set_mats[2][c], "res")):
-                split = mat.split(1) if kind != "silu" else 1
+                split = mat.split(1) if kind == "res" else 1
                 if (mat.rows, split) not in self.parts:
                     self.parts[(mat.rows, split)] = torch.empty(split, 1, mat.rows, device="cuda")
                 self.launches.append((mat, kind, self.parts[(mat.rows, split)]))
 
     def run(self, stream=None):
-        from qwenny_amd import Epi, add_rmsnorm, sum_parts
+        from qwenny_amd import Epi, add_rmsnorm
 
         for mat, kind, y in self.launches:
             if kind == "silu":
                 self.gemm.run(stream, 1, mat, self.x, self.mid, Epi.Silu)
                 continue
-            split = self.gemm.run(stream, 1, mat, self.x, y, Epi.Plain)
             if kind == "in":
-                sum_parts(stream, y, split, 1, mat.rows, self.ys)
-            else:
-                add_rmsnorm(stream, self.h, y, split, 1, 5120, self.w, self.yb)
+                self.gemm.run_split(stream, 1, mat, self.x, y, Epi.Plain, True)
+                continue
+            split = self.gemm.run(stream, 1, mat, self.x, y, Epi.Plain)
+            add_rmsnorm(stream, self.h, y, split, 1, 5120, self.w, self.yb)
 
     def bytes(self):
         k, n = 5120, 2 * 17408  # [gate; up]: int4 codes and scales, x once, bf16 output of n / 2 rows
@@ -909,6 +909,25 @@ def main():
         extra["m1_with_sums"] = {"GBps": round(sst.bytes() / (sms * 1e-3) / 1e9, 1), "ms_per_step": round(sms, 5)}
         print(f"# M=1 27B set x4 + head, each plain product's partials summed: {sms:.4f} ms/step, "
               f"{sst.bytes() / (sms * 1e-3) / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+        # the same step with each plain product asked for whole rows (one partial, as the reference's int4 products
+        # return): the workgroup-per-tile-pair kernel, its sums met in LDS
+        wst = decode_step(1)
+        wys = {}
+
+        def run_whole(stream=None):
+            for mat, epi, y, _, _ in wst.launches:
+                if epi == Epi.Argmax:
+                    gemm.run(stream, 1, mat, wst.x, y, epi, n_out=1, keys=wst.keys)
+                    continue
+                if mat.rows not in wys:
+                    wys[mat.rows] = torch.empty(mat.rows, dtype=torch.float32, device="cuda")
+                gemm.run_split(stream, 1, mat, wst.x, wys[mat.rows], epi, True)
+
+        wst.run = run_whole
+        wms = time_step(wst, args.steps, args.warmup, not args.no_graph)
+        extra["m1_whole_rows"] = {"GBps": round(wst.bytes() / (wms * 1e-3) / 1e9, 1), "ms_per_step": round(wms, 5)}
+        print(f"# M=1 27B set x4 + head, each plain product as whole rows: {wms:.4f} ms/step, "
+              f"{wst.bytes() / (wms * 1e-3) / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
     if "m5" in only:
         st5 = decode_step(5)
         ms5 = time_step(st5, args.steps, args.warmup, not args.no_graph)

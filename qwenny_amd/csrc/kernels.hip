@@ -782,12 +782,12 @@ static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
     }
 }
 
-// skinny_m1w_kernel: one-token products that need whole sums (the SwiGLU epilogue; argmax too, not dispatched) of
-// int4 with bf16
-// scales, symmetric or with zero points, no adapter, on the lean terms of skinny_m1_kernel: a workgroup takes one
-// pair of tiles over all of K, one wave per 4-group chunk (WK = G / 4 <= 16 waves), each as short-lived as a plain
-// product's; the chunks' sums meet in LDS and the first wave adds them in chunk order. (skinny_kernel runs these with
-// 2 x 2-wave workgroups whose waves each walk G / 8 chunks, one after another.)
+// skinny_m1w_kernel: one-token products that need whole sums (the SwiGLU epilogue, plain products asked for whole
+// rows; argmax too, not dispatched) of int4 with bf16 scales, symmetric or with zero points, no adapter, on the lean
+// terms of skinny_m1_kernel: a workgroup takes one pair of tiles over all of K, one wave per 4-group chunk (WK = G / 4
+// waves when that is at most 16; else each wave takes every WK-th chunk, WK = ceil(chunks / ceil(chunks / 16))), each
+// chunk as short-lived as a plain product's wave; the waves' sums meet in LDS and the first wave adds them in wave
+// order. (skinny_kernel runs these with 2 x 2-wave workgroups whose waves each walk G / 8 chunks, one after another.)
 struct M1wArgs {
     const u32x4* codes;
     const uint16_t* scales;
@@ -808,52 +808,56 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
     const int WK = blockDim.x >> 6;
     const int l16 = lane & 15, kq = lane >> 4;
     const int T = a.tiles, G = a.G;
-    const int tile0 = blockIdx.x * 2, gw = 4 * wk;
+    const int tile0 = blockIdx.x * 2;
     const int t1 = min(tile0 + 1, T - 1);
     __bf16* xw = (__bf16*)smem + wk * 4 * QG;
-    float* red = (float*)(smem + (size_t)WK * 4 * QG * 2);  // [WK][32]: each chunk's sums of the 32 rows
+    float* red = (float*)(smem + (size_t)WK * 4 * QG * 2);  // [WK][32]: each wave's sums of the 32 rows
     uint32_t magic;
     asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
     const uint32_t mask = a.mask;
-    __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)gw * QG + 8 * lane),
-                                     (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t sraw[2][2], zraw[2];
     const int tl[2] = {tile0, t1};
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const unsigned long long v =
-            __builtin_nontemporal_load((const unsigned long long*)(a.scales + scale_idx(tl[t], T, gw, l16)));
-        sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
-        if (ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tl[t], T, gw, l16));
-    }
-    u32x4 code[4][2];
-#pragma unroll
-    for (int gi = 0; gi < 4; gi++)
-#pragma unroll
-        for (int t = 0; t < 2; t++) code[gi][t] = __builtin_nontemporal_load(a.codes + ((size_t)tl[t] * G + gw + gi) * 64 + lane);
-    constexpr int WL = 2 + (ZP ? 2 : 0) + 8;
-    __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
-    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
     float acc[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int gi = 0; gi < 4; gi++) {
-        u32x4 xa[4];
-        const __bf16* xrow = xw + gi * QG + 8 * kq;
-#pragma unroll
-        for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow + 32 * j);
-        f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
+    // the wave's chunks of 4 groups: wk, wk + WK, ... (one when K has at most 16 chunks)
+    for (int gw = 4 * wk; gw < G; gw += 4 * WK) {
+        __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)gw * QG + 8 * lane),
+                                         (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t sraw[2][2], zraw[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+            const unsigned long long v =
+                __builtin_nontemporal_load((const unsigned long long*)(a.scales + scale_idx(tl[t], T, gw, l16)));
+            sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
+            if (ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tl[t], T, gw, l16));
+        }
+        u32x4 code[4][2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) d = mfma(xa[j], i4_biased(code[gi][t][j], mask, magic), d);
-            const uint32_t w = sraw[t][gi >> 1];
-            const float sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
-            const float cz = ZP ? (float)(128 + (int)((zraw[t] >> (4 * gi)) & 15u)) : 136.0f;
-            acc[t] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[0], d[0]), acc[t]);
+        for (int gi = 0; gi < 4; gi++)
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+                code[gi][t] = __builtin_nontemporal_load(a.codes + ((size_t)tl[t] * G + gw + gi) * 64 + lane);
+        constexpr int WL = 2 + (ZP ? 2 : 0) + 8;
+        __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
+        const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            u32x4 xa[4];
+            const __bf16* xrow = xw + gi * QG + 8 * kq;
+#pragma unroll
+            for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow + 32 * j);
+            f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; j++) d = mfma(xa[j], i4_biased(code[gi][t][j], mask, magic), d);
+                const uint32_t w = sraw[t][gi >> 1];
+                const float sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
+                const float cz = ZP ? (float)(128 + (int)((zraw[t] >> (4 * gi)) & 15u)) : 136.0f;
+                acc[t] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[0], d[0]), acc[t]);
+            }
         }
     }
     if (kq == 0) {
@@ -870,6 +874,8 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
         if (EPI == EPI_SILU) {
             const float up = __shfl_xor(v, 8);  // rows 8..15 of a tile are the up rows of rows 0..7
             if (ok && l16 < 8) ((__bf16*)a.y)[tile * 8 + l16] = (__bf16)(silu(v) * up);
+        } else if (EPI == EPI_PLAIN) {
+            if (ok) ((float*)a.y)[out] = v;
         } else {
             unsigned long long k = 0;
             if (ok) {
@@ -1593,6 +1599,20 @@ static hipError_t skinny_epi(const Launch& l) {
         const int G = l.cols / QG;
         if (l.m == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && G / 4 <= 16) {
             const int tiles = l.rows / TILE, wk = G / 4;
+            const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
+                            l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
+            const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
+            hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
+                               a);
+            return hipGetLastError();
+        }
+    }
+    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
+        // one token, whole rows (split 1): the workgroup-per-tile-pair kernel, its waves taking one or more chunks of
+        // 4 groups each (at most 16 waves)
+        const int G = l.cols / QG;
+        if (l.m == 1 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && !l.stage_out) {
+            const int tiles = l.rows / TILE, nc = G / 4, per = (nc + 15) / 16, wk = (nc + per - 1) / per;
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
                             l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;

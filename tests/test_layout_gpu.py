@@ -145,6 +145,20 @@ def test_whole(gemm, kind, m):
     assert rel_err(whole, _plain(gemm, mat, x, m)) <= 1e-5
 
 
+@pytest.mark.parametrize("kind,k", [("i4", 17408), ("i4z", 17408), ("i4", 9216), ("i4z", 2560)])
+def test_whole_one_token_long_k(gemm, kind, k):
+    """run_split(whole) at one token on the workgroup-per-tile-pair kernel, whose waves take one or several chunks of
+    4 groups of K (17408: 34 chunks over 12 waves, 10 of them taking 3; 9216: 18 over 9): every row against the
+    oracle, and the split product's value. 35 tiles: the last tile pair is half empty."""
+    print(f"whole one-token {kind} k={k}", flush=True)
+    q = make_quant(79, kind, 560, k)
+    x = activations(15, "x", 1, k)
+    mat = Mat.stack(gemm, [q])
+    whole = _plain(gemm, mat, x, 1, whole=True)
+    assert rel_err(whole, oracle_y(q, x)) <= 1e-4
+    assert rel_err(whole, _plain(gemm, mat, x, 1)) <= 1e-5
+
+
 def test_part_len(gemm):
     mats = [Mat.stack(gemm, [make_quant(78, "i4", 256, k)]) for k in (512, 4096)]
     for max_tok in (16, SKINNY_MAX_M, SKINNY_MAX_M + 1, 300, 600):
