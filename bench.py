@@ -882,6 +882,27 @@ def main():
     print(f"# roofline kernel (plain M=1 set): {per_launch_s * 1e6:.2f} us per launch, "
           f"{per_launch_bytes / per_launch_s / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 
+    def whole_rows_step(m):
+        """The decode step with each plain product asked for whole rows (one partial, as the reference's int4 products
+        return): the workgroup-per-tile-pair kernels, their sums met in LDS."""
+        wst = decode_step(m)
+        wys = {}
+
+        def run_whole(stream=None):
+            for mat, epi, y, _, _ in wst.launches:
+                if epi == Epi.Argmax:
+                    gemm.run(stream, m, mat, wst.x, y, epi, n_out=m, keys=wst.keys)
+                    continue
+                if mat.rows not in wys:
+                    wys[mat.rows] = torch.empty(m * mat.rows, dtype=torch.float32, device="cuda")
+                gemm.run_split(stream, m, mat, wst.x, wys[mat.rows], epi, True)
+
+        wst.run = run_whole
+        wms = time_step(wst, args.steps, args.warmup, not args.no_graph)
+        print(f"# M={m} 27B set x4 + head, each plain product as whole rows: {wms:.4f} ms/step, "
+              f"{wst.bytes() / (wms * 1e-3) / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+        return {"GBps": round(wst.bytes() / (wms * 1e-3) / 1e9, 1), "ms_per_step": round(wms, 5)}
+
     extra = {}
     floor = read_floor(set_mats, args)
     extra["read_floor"] = floor
@@ -909,30 +930,14 @@ def main():
         extra["m1_with_sums"] = {"GBps": round(sst.bytes() / (sms * 1e-3) / 1e9, 1), "ms_per_step": round(sms, 5)}
         print(f"# M=1 27B set x4 + head, each plain product's partials summed: {sms:.4f} ms/step, "
               f"{sst.bytes() / (sms * 1e-3) / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
-        # the same step with each plain product asked for whole rows (one partial, as the reference's int4 products
-        # return): the workgroup-per-tile-pair kernel, its sums met in LDS
-        wst = decode_step(1)
-        wys = {}
-
-        def run_whole(stream=None):
-            for mat, epi, y, _, _ in wst.launches:
-                if epi == Epi.Argmax:
-                    gemm.run(stream, 1, mat, wst.x, y, epi, n_out=1, keys=wst.keys)
-                    continue
-                if mat.rows not in wys:
-                    wys[mat.rows] = torch.empty(mat.rows, dtype=torch.float32, device="cuda")
-                gemm.run_split(stream, 1, mat, wst.x, wys[mat.rows], epi, True)
-
-        wst.run = run_whole
-        wms = time_step(wst, args.steps, args.warmup, not args.no_graph)
-        extra["m1_whole_rows"] = {"GBps": round(wst.bytes() / (wms * 1e-3) / 1e9, 1), "ms_per_step": round(wms, 5)}
-        print(f"# M=1 27B set x4 + head, each plain product as whole rows: {wms:.4f} ms/step, "
-              f"{wst.bytes() / (wms * 1e-3) / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+        extra["m1_whole_rows"] = whole_rows_step(1)
     if "m5" in only:
         st5 = decode_step(5)
         ms5 = time_step(st5, args.steps, args.warmup, not args.no_graph)
         extra["m5_GBps"] = round(st5.bytes() / (ms5 * 1e-3) / 1e9, 1)
         print(f"# M=5: {ms5:.4f} ms/step, {extra['m5_GBps']} GB/s", file=sys.stderr, flush=True)
+        if "m1sum" in only:
+            extra["m5_whole_rows"] = whole_rows_step(5)
     if "prefill" in only:
         pf = {}
         for i, (k, n) in enumerate(PREFILL_27B):

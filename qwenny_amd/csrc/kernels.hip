@@ -1010,6 +1010,96 @@ static __global__ __launch_bounds__(512) void skinny_mt_kernel(MtArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// skinny_mw_kernel: whole rows (split 1) of a plain product of 2-8 tokens, int4 with bf16 scales, symmetric or with
+// zero points, no adapter: skinny_m1w_kernel's partition (a workgroup per tile pair over all of K, each wave taking
+// every WK-th chunk of 4 groups) with skinny_mt_kernel's arithmetic (each wave stages its tokens' rows of its chunk,
+// 16 bytes apart; token 4 (lane / 16) + r in row r of a lane's accumulators). The waves' sums meet in LDS and the
+// first wave adds them in wave order.
+template <bool ZP, int NR>
+static __global__ __launch_bounds__(1024) void skinny_mw_kernel(MtArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int XP = mt_xpitch<4>();
+    const int lane = threadIdx.x & 63, wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int WK = blockDim.x >> 6;
+    const int l16 = lane & 15, kq = lane >> 4;
+    const int T = a.tiles, G = a.G, M = a.m;
+    const int tile0 = blockIdx.x * 2, t1 = min(tile0 + 1, T - 1);
+    __bf16* xw = (__bf16*)smem + (size_t)wk * M * XP;                // the wave's M staged rows
+    float* red = (float*)(smem + (size_t)WK * M * XP * 2);          // [WK][M][32]: each wave's sums
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
+    const uint32_t mask = a.mask;
+    const int tl[2] = {tile0, t1};
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    float acc[2][NR];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) acc[t][r] = 0.0f;
+    const __bf16* xrow0 = xw + min(l16, M - 1) * XP + 8 * kq;  // rows past M read row M - 1 (never stored)
+    for (int gw = 4 * wk; gw < G; gw += 4 * WK) {
+        for (int r = 0; r < M; r++)
+            __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)r * a.ldx + (size_t)gw * QG + 8 * lane),
+                                             (__attribute__((address_space(3))) void*)(xw + r * XP), 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t sraw[2][2], zraw[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const unsigned long long v =
+                __builtin_nontemporal_load((const unsigned long long*)(a.scales + scale_idx(tl[t], T, gw, l16)));
+            sraw[t][0] = (uint32_t)v, sraw[t][1] = (uint32_t)(v >> 32);
+            if (ZP) zraw[t] = __builtin_nontemporal_load(a.zeros + zero_idx(tl[t], T, gw, l16));
+        }
+        u32x4 code[4][2];
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++)
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+                code[gi][t] = __builtin_nontemporal_load(a.codes + ((size_t)tl[t] * G + gw + gi) * 64 + lane);
+        // the activations landed (the weight loads issued after them may stay in flight)
+        constexpr int WL = 2 + (ZP ? 2 : 0) + 8;
+        __builtin_amdgcn_s_waitcnt((WL & 15) | ((WL >> 4) << 14) | (7 << 4) | (15 << 8));
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            u32x4 xa[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) xa[j] = *(const u32x4*)(xrow0 + gi * QG + 32 * j);
+            f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) xsum = mfma(xa[j], ones, xsum);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; j++) d = mfma(xa[j], i4_biased(code[gi][t][j], mask, magic), d);
+                const uint32_t w = sraw[t][gi >> 1];
+                const float sc = __uint_as_float((gi & 1) ? (w & 0xffff0000u) : (w << 16));
+                const float cz = ZP ? (float)(128 + (int)((zraw[t] >> (4 * gi)) & 15u)) : 136.0f;
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-cz, xsum[r], d[r]), acc[t][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const int tok = 4 * kq + r;
+            if (tok < M) red[(wk * M + tok) * 32 + t * TILE + l16] = acc[t][r];
+        }
+    __syncthreads();
+    if (wk == 0) {
+        const int rows = T * TILE;
+        for (int i = lane; i < M * 32; i += 64) {
+            const int tok = i >> 5, row = i & 31, tile = tile0 + (row >> 4);
+            float v = 0.0f;
+            for (int c = 0; c < WK; c++) v += red[(c * M + tok) * 32 + row];
+            if (tile < T) __builtin_nontemporal_store(v, a.y + (size_t)tok * rows + tile * TILE + (row & 15));
+        }
+    }
+}
+
 // prefill_kernel
 //
 // On v_mfma_f32_32x32x16_bf16 (on gfx950 it sustains about twice the rate of the 16x16x32 form). A: 32 tokens x 16
@@ -1618,6 +1708,21 @@ static hipError_t skinny_epi(const Launch& l) {
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
             hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
                                a);
+            return hipGetLastError();
+        }
+    }
+    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
+        // 2-8 tokens, whole rows: the same partition with the multi-token arithmetic
+        const int G = l.cols / QG;
+        if (l.m >= 2 && l.m <= 8 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0) {
+            const int tiles = l.rows / TILE, nc = G / 4, per = (nc + 15) / 16, wk = (nc + per - 1) / per;
+            const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
+                           (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
+            const size_t lds = (size_t)wk * l.m * mt_xpitch<4>() * 2 + (size_t)wk * l.m * 32 * 4;
+            const dim3 grid((tiles + 1) / 2), block(64 * wk);
+            if (l.m == 2) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 2>), grid, block, lds, l.stream, a);
+            else if (l.m == 3) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 3>), grid, block, lds, l.stream, a);
+            else hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 4>), grid, block, lds, l.stream, a);
             return hipGetLastError();
         }
     }

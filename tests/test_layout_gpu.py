@@ -145,18 +145,19 @@ def test_whole(gemm, kind, m):
     assert rel_err(whole, _plain(gemm, mat, x, m)) <= 1e-5
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
 @pytest.mark.parametrize("kind,k", [("i4", 17408), ("i4z", 17408), ("i4", 9216), ("i4z", 2560)])
-def test_whole_one_token_long_k(gemm, kind, k):
-    """run_split(whole) at one token on the workgroup-per-tile-pair kernel, whose waves take one or several chunks of
-    4 groups of K (17408: 34 chunks over 12 waves, 10 of them taking 3; 9216: 18 over 9): every row against the
+def test_whole_decode_long_k(gemm, kind, k, m):
+    """run_split(whole) at 1-8 tokens on the workgroup-per-tile-pair kernels, whose waves take one or several chunks
+    of 4 groups of K (17408: 34 chunks over 12 waves, 10 of them taking 3; 9216: 18 over 9): every row against the
     oracle, and the split product's value. 35 tiles: the last tile pair is half empty."""
-    print(f"whole one-token {kind} k={k}", flush=True)
+    print(f"whole decode {kind} k={k} m={m}", flush=True)
     q = make_quant(79, kind, 560, k)
-    x = activations(15, "x", 1, k)
+    x = activations(15 + m, "x", m, k)
     mat = Mat.stack(gemm, [q])
-    whole = _plain(gemm, mat, x, 1, whole=True)
+    whole = _plain(gemm, mat, x, m, whole=True)
     assert rel_err(whole, oracle_y(q, x)) <= 1e-4
-    assert rel_err(whole, _plain(gemm, mat, x, 1)) <= 1e-5
+    assert rel_err(whole, _plain(gemm, mat, x, m)) <= 1e-5
 
 
 def test_part_len(gemm):
