@@ -1678,6 +1678,17 @@ static hipError_t skinny_nr(const Launch& l) {
         return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4, TB>(l) : skinny_ng<F, EPI, NR, 1, TB>(l);
 }
 
+// Waves per workgroup of the workgroup-per-tile-pair kernels for nc chunks of K and wgs workgroups: one chunk each
+// when at most 16, else ceil(nc / 16) chunks each; two chunks each when one would not fit the grid in one round of
+// resident workgroups (two 10-wave workgroups per CU at their 80 registers): at 5 tokens, (5120, 17408) 14.5 -> 12.5 us
+// (at one token, and for the one-token SwiGLU, the same within 1%), while on grids of one round the longer waves lost
+// 10-20%.
+static int mw_waves(int nc, int wgs, int cus) {
+    int per = (nc + 15) / 16;
+    if (per == 1 && nc >= 2 && wgs > std::max(1, 24 / nc) * cus) per = 2;
+    return (nc + per - 1) / per;
+}
+
 // token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
@@ -1688,7 +1699,7 @@ static hipError_t skinny_epi(const Launch& l) {
         // with a returning atomic, made it 20% slower (106 -> 128 us).
         const int G = l.cols / QG;
         if (l.m == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && G / 4 <= 16) {
-            const int tiles = l.rows / TILE, wk = G / 4;
+            const int tiles = l.rows / TILE, wk = mw_waves(G / 4, (tiles + 1) / 2, l.cus);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
                             l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
@@ -1702,7 +1713,7 @@ static hipError_t skinny_epi(const Launch& l) {
         // 4 groups each (at most 16 waves)
         const int G = l.cols / QG;
         if (l.m == 1 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && !l.stage_out) {
-            const int tiles = l.rows / TILE, nc = G / 4, per = (nc + 15) / 16, wk = (nc + per - 1) / per;
+            const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
                             l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
@@ -1715,7 +1726,7 @@ static hipError_t skinny_epi(const Launch& l) {
         // 2-8 tokens, whole rows: the same partition with the multi-token arithmetic
         const int G = l.cols / QG;
         if (l.m >= 2 && l.m <= 8 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0) {
-            const int tiles = l.rows / TILE, nc = G / 4, per = (nc + 15) / 16, wk = (nc + per - 1) / per;
+            const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
             const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
                            (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
             const size_t lds = (size_t)wk * l.m * mt_xpitch<4>() * 2 + (size_t)wk * l.m * 32 * 4;
