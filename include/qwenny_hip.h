@@ -281,6 +281,20 @@ int qh_lora_silu(void* stream, const float* xa, int split, int m_cols, const uin
                  const int32_t* tab, const int32_t* tok_slot, const float* slot_scale, size_t n, const float* y,
                  size_t ldy, void* mid_bf16);
 
+/* ---- graph capture --------------------------------------------------------------------------------------------- */
+
+/* Replaces the capture and replay inside Graphs::run (src/cuda/core.rs:1151-1192); the graph cache around it (keys,
+ * LRU, memory floor) stays with the caller. The launches the calling thread makes on `stream` (not the null stream)
+ * between qh_graph_begin and qh_graph_end become one graph (thread-local capture mode), instantiated for replay with
+ * qh_graph_launch on any stream; qh_graph_free releases it. Every launch entry point of this library may be captured:
+ * none allocates, synchronises or records a memset. Buffers and arguments are those of the capture at every replay;
+ * argmax keys keep their running maximum, so a caller resets them between replays as between eager calls. */
+typedef struct qh_graph qh_graph;
+int qh_graph_begin(void* stream);
+int qh_graph_end(void* stream, qh_graph** out);
+int qh_graph_launch(const qh_graph* g, void* stream);
+void qh_graph_free(qh_graph* g);
+
 /* ---- measurement aid ------------------------------------------------------------------------------------------ */
 
 /* No counterpart in the reference: a read-only kernel for the benchmark and its profiles. It reads `tiles` x `groups`

@@ -5,9 +5,9 @@ products, and the dense 16-bit products of the same call sites, in hand-written 
 mirror of the reference's `Mat` / `Gemm` runtime and checkpoint formats.
 """
 
-from .core import (SKINNY_MAX_M, Epi, Gemm, Mat, Quant, Wt, add_rmsnorm, dequant, lora_add, lora_silu, pack_dense_bf16,
+from .core import (SKINNY_MAX_M, Epi, Gemm, Graph, Mat, Quant, Wt, add_rmsnorm, dequant, lora_add, lora_silu, pack_dense_bf16,
                    pack_dense_int8, pack_quant, packed_sizes, row_order, sum_parts, unpack_rows, unpack_rows_bf16)
 
-__all__ = ["SKINNY_MAX_M", "Epi", "Gemm", "Mat", "Quant", "Wt", "add_rmsnorm", "dequant", "lora_add", "lora_silu",
+__all__ = ["SKINNY_MAX_M", "Epi", "Gemm", "Graph", "Mat", "Quant", "Wt", "add_rmsnorm", "dequant", "lora_add", "lora_silu",
            "pack_dense_bf16", "pack_dense_int8", "pack_quant", "packed_sizes", "row_order", "sum_parts", "unpack_rows",
            "unpack_rows_bf16"]

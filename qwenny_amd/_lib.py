@@ -52,6 +52,10 @@ SIGNATURES = {
     "qh_quant_to_bf16": (I, [ctypes.POINTER(QuantC), P]),
     "qh_dequant": (I, [P, P, P, P, S, S, S, I, I, S, S, P, I]),
     "qh_diag_read": (I, [P, P, S, S, I, P]),
+    "qh_graph_begin": (I, [P]),
+    "qh_graph_end": (I, [P, ctypes.POINTER(P)]),
+    "qh_graph_launch": (I, [P, P]),
+    "qh_graph_free": (None, [P]),
     "qh_sum_parts": (I, [P, P, I, S, S, P]),
     "qh_add_rmsnorm": (I, [P, P, P, I, S, S, P, P, ctypes.c_float]),
     "qh_lora_add": (I, [P, P, I, I, P, I, S, P, P, P, S, P, S]),

@@ -16,7 +16,7 @@ BUILD = os.path.join(HERE, "_build")
 ARCH = os.environ.get("QWENNY_ARCH", "gfx950")
 
 HOST_SRC = ["host.cpp"]
-HIP_SRC = ["api.hip", "noalloc.hip", "dequant.hip", "consumers.hip", "diag.hip"]
+HIP_SRC = ["api.hip", "noalloc.hip", "dequant.hip", "consumers.hip", "diag.hip", "graph.hip"]
 # kernels.hip is compiled once per (storage format, epilogue) pair and once for the dispatcher, in parallel; the
 # formats are the F_* combinations that kernels.hip's launch() dispatches.
 KERNEL_FORMATS = {"i4": 0, "i4s32": 4, "zp": 2, "zps32": 6, "i8": 5, "i8perch": 13, "bf16": 16}

@@ -449,3 +449,43 @@ def pack_dense_int8(w_bf16, order):
     check(lib().qh_pack_dense_int8(_np_ptr(w), w.shape[0], w.shape[1], _np_ptr(order), order.size, _np_ptr(codes),
                                    _np_ptr(scales)))
     return codes, scales
+
+
+class Graph:
+    """A captured sequence of launches (the capture and replay inside src/cuda/core.rs:1151-1192 `Graphs::run`):
+
+        g = Graph.capture(stream, lambda: gemm.run(stream, ...))
+        g.launch(stream)
+
+    `stream`: a torch stream (not the null stream) or a hipStream_t as an int."""
+
+    def __init__(self, handle):
+        self._g = handle
+
+    @classmethod
+    def capture(cls, stream, fn):
+        s = _stream(stream)
+        check(lib().qh_graph_begin(s))
+        h = P()
+        try:
+            fn()
+        except BaseException:
+            if lib().qh_graph_end(s, ctypes.byref(h)) == 0:  # the capture ends either way
+                lib().qh_graph_free(h)
+            raise
+        check(lib().qh_graph_end(s, ctypes.byref(h)))
+        return cls(h)
+
+    def launch(self, stream):
+        check(lib().qh_graph_launch(self._g, _stream(stream)))
+
+    def close(self):
+        if self._g:
+            lib().qh_graph_free(self._g)
+            self._g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

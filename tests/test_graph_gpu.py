@@ -158,3 +158,62 @@ def test_graph_consumers_replay(gemm):
         torch.cuda.synchronize()
         for a, b_ in zip(outs(), want):
             assert np.array_equal(a, b_), rep
+
+
+def test_abi_graph_capture_replays(gemm):
+    """The library's own capture entry points (qh_graph_begin / end / launch / free, through qwenny_amd.Graph) over a
+    step that also holds the whole-row decode kernels (one and five tokens), the one-token SwiGLU product and the
+    prefill SwiGLU product with its f16 activation conversion: every replay, with new inputs and eager launches
+    between replays, equals the eager step bit for bit."""
+    import torch
+
+    from qwenny_amd import Graph
+    from qwenny_amd._lib import QhError
+
+    print("graph capture through the C ABI", flush=True)
+    k = 5120
+    dec = Mat.stack(gemm, [make_quant(96, "i4", 2048, k)])
+    gu_q = [make_quant(97, "i4", 1024, k), make_quant(98, "i4z", 1024, k)]
+    gu = Mat.stack(gemm, gu_q, silu=True)
+    x1 = torch.empty((1, k), dtype=torch.bfloat16, device="cuda")
+    x5 = torch.empty((256, k), dtype=torch.bfloat16, device="cuda")
+    y_w1 = torch.empty((1, dec.rows), dtype=torch.float32, device="cuda")
+    y_w5 = torch.empty((5, dec.rows), dtype=torch.float32, device="cuda")
+    y_s1 = torch.empty((1, gu.rows // 2), dtype=torch.bfloat16, device="cuda")
+    y_s256 = torch.empty((256, gu.rows // 2), dtype=torch.bfloat16, device="cuda")
+    outs = (y_w1, y_w5, y_s1, y_s256)
+
+    def step(stream):
+        assert gemm.run_split(stream, 1, dec, x1, y_w1, Epi.Plain, True) == 1
+        assert gemm.run_split(stream, 5, dec, x5, y_w5, Epi.Plain, True) == 1
+        gemm.run(stream, 1, gu, x1, y_s1, Epi.Silu)
+        gemm.run(stream, 256, gu, x5, y_s256, Epi.Silu)
+
+    def load(seed):
+        x1.copy_(to_dev(activations(seed, "x", 1, k)))
+        x5.copy_(to_dev(activations(seed + 1, "x", 256, k)))
+
+    load(1)
+    step(None)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with pytest.raises(QhError):
+        Graph.capture(0, lambda: None)  # the null stream cannot be captured
+    g = Graph.capture(s, lambda: step(s))
+    try:
+        for rep in range(3):
+            load(20 + 2 * rep)
+            torch.cuda.synchronize()
+            step(None)
+            torch.cuda.synchronize()
+            want = [t.float().cpu().numpy().copy() for t in outs]
+            for t in outs:
+                t.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.launch(s)
+            s.synchronize()
+            got = [t.float().cpu().numpy() for t in outs]
+            for a, b in zip(got, want):
+                assert np.array_equal(a, b), rep
+    finally:
+        g.close()
