@@ -1159,9 +1159,10 @@ __device__ __forceinline__ int pf_lds_off(int row, int kc) { return row * PF_ROW
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // 16 bytes per lane global -> LDS (global_load_lds_dwordx4: wave-uniform base + 32-bit lane offset) into the 1 KiB at
-// dst. In inline assembly: the compiler counts its own form of this load against the LDS counter as well and makes the
-// wave's next LDS read wait for the global load to complete (a whole memory round trip before the ping-pong's MFMA
-// phase); the hardware's LDS reads are ordered by the workgroup barriers that already follow every stage's loads.
+// dst. In inline assembly: with its own form of this load in flight the compiler cannot order the wave's LDS reads
+// against it and waits for every outstanding LDS operation (lgkmcnt(0)) at the next read's use, which in the
+// ping-pong's MFMA phase drains the A-fragment ring before the first MFMA. The data's readers are ordered by the
+// s_waitcnt and workgroup barrier that follow every stage's loads.
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, lds_ptr dst) {
     // both wave-uniform by construction; read from the first lane so that they are in scalar registers whatever the
     // compiler could prove
