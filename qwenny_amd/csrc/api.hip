@@ -360,7 +360,6 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
     l.ldy = (int)(epi == QH_EPI_SILU ? w->rows / 2 : w->rows);
     l.keys = (unsigned long long*)keys;
     l.argmax_table = (unsigned long long*)sc.argmax;
-    l.argmax_count = (unsigned*)((uint8_t*)sc.argmax + ARGMAX_SPREAD * ARGMAX_MAX_TOK * 8);
     l.epi = epi;
     l.stream = (hipStream_t)stream;
     l.bf16_magic = 0x43004300u;

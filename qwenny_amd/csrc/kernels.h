@@ -31,7 +31,6 @@ struct Launch {
     int ldy;                // elements between y rows
     unsigned long long* keys;
     unsigned long long* argmax_table;  // [ARGMAX_SPREAD][ARGMAX_MAX_TOK], zero between launches
-    unsigned* argmax_count;            // workgroups done, zero between launches
     int epi;                // enum qh_epi
     int split;              // grid split-K (plain products only)
     int waves;              // waves per workgroup (skinny kernel): tile_waves over tiles x waves / tile_waves over K
@@ -112,8 +111,8 @@ size_t skinny_lds(const Launch& l);
 
 enum { EPI_PLAIN = 0, EPI_SILU = 1, EPI_ARGMAX = 2 };
 
-// Scratch of a product launch: the argmax table (ARGMAX_SPREAD x ARGMAX_MAX_TOK u64) followed by its workgroup counter
-// (ARGMAX_SCRATCH_BYTES in all), and the stream-K partials (PF_SK_PART_BYTES) followed by PF_SK_ITEMS_MAX item counters
+// Scratch of a product launch: the argmax table (ARGMAX_SPREAD x ARGMAX_MAX_TOK u64, and 256 bytes more:
+// ARGMAX_SCRATCH_BYTES in all), and the stream-K partials (PF_SK_PART_BYTES) followed by PF_SK_ITEMS_MAX item counters
 // (PF_SK_SCRATCH_BYTES in all); every counter and table entry zero between launches.
 struct Scratch {
     void* argmax;

@@ -129,15 +129,13 @@ __device__ __forceinline__ unsigned long long group16_max(unsigned long long k) 
 }
 
 // The argmax across workgroups without every workgroup hitting the same cache line of keys[]: a workgroup folds its
-// per-token maxima into one of ARGMAX_SPREAD rows of a scratch table (row = its index mod ARGMAX_SPREAD), and the last
-// workgroup of the launch folds the table into keys[] (one atomicMax per token), zeroing it as it reads, and resets
-// the workgroup counter: the next launch (or graph replay) starts from a clean table. One launch at a time per
-// context uses the table (launches on one stream).
-//
-// Ordering uses device-scope atomics only, no release fences: a fence at device scope writes back the XCD's L2 on
-// this part, far too costly once per workgroup. Every table and counter update is a returning device-scope atomic
-// (performed at the device's coherence point); a workgroup waits for its own to return before it counts itself done,
-// and the last workgroup reads the table with atomic exchanges after its count returned.
+// per-token maxima into one of ARGMAX_SPREAD rows of a scratch table (row = its index mod ARGMAX_SPREAD) with
+// non-returning device-scope atomics, and a one-workgroup kernel launched right after the product on the same stream
+// (argmax_fold_kernel; the kernel boundary orders the table updates before its reads) folds the table into keys[]
+// (one atomicMax per token), zeroing it as it reads: the next launch (or graph replay) starts from a clean table. One
+// product at a time per context uses the table (launches on one stream). Against a last-workgroup protocol in the
+// product itself (each workgroup's table updates returned, then a returning count on one counter), the extra launch
+// measured faster: the 27B head 3.8 us per step less.
 __device__ __forceinline__ void argmax_spread_max(unsigned long long* table, int tok, unsigned long long k) {
     const int row = (blockIdx.y * gridDim.x + blockIdx.x) % ARGMAX_SPREAD;
     (void)__hip_atomic_fetch_max(table + row * ARGMAX_MAX_TOK + tok, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -146,31 +144,27 @@ __device__ __forceinline__ void argmax_spread_max(const Launch& a, int tok, unsi
     argmax_spread_max(a.argmax_table, tok, k);
 }
 
-__device__ void argmax_finish(unsigned long long* table, unsigned* count, unsigned long long* keys, int m, int tid,
-                              int nthr) {
-    __shared__ int last;
+static __global__ __launch_bounds__(256) void argmax_fold_kernel(unsigned long long* table, unsigned long long* keys,
+                                                                 int m) {
     __shared__ unsigned long long best[ARGMAX_MAX_TOK];
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's table updates have returned
+    for (int t = threadIdx.x; t < m; t += blockDim.x) best[t] = 0;
     __syncthreads();
-    if (tid == 0)
-        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               gridDim.x * gridDim.y - 1;
-    for (int t = tid; t < m; t += nthr) best[t] = 0;
-    __syncthreads();
-    if (!last) return;  // uniform over the workgroup
-    for (int i = tid; i < ARGMAX_SPREAD * m; i += nthr) {
+    // read and cleared at the coherence point where the product's atomics were performed (agent-scope exchanges)
+    for (int i = threadIdx.x; i < ARGMAX_SPREAD * m; i += blockDim.x) {
         const int row = i / m, tok = i - row * m;
         const unsigned long long k =
             __hip_atomic_exchange(table + row * ARGMAX_MAX_TOK + tok, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (k) atomicMax(best + tok, k);
     }
     __syncthreads();
-    for (int t = tid; t < m; t += nthr)
+    for (int t = threadIdx.x; t < m; t += blockDim.x)
         if (best[t]) (void)__hip_atomic_fetch_max(keys + t, best[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid == 0) (void)__hip_atomic_exchange(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ void argmax_finish(const Launch& a, int tid, int nthr) {
-    argmax_finish(a.argmax_table, a.argmax_count, a.keys, a.m, tid, nthr);
+
+// the fold after an argmax product's launch (m logit rows)
+static hipError_t argmax_fold(const Launch& l, int m) {
+    hipLaunchKernelGGL(argmax_fold_kernel, dim3(1), dim3(256), 0, l.stream, l.argmax_table, l.keys, m);
+    return hipGetLastError();
 }
 
 // Words of a (tile, group) code block per lane (16 bytes each).
@@ -682,7 +676,6 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
                 const int tok = 16 * b + 4 * kq + r;
                 if (lead && l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
             }
-        argmax_finish(a, tid, nthr);
     }
 }
 
@@ -783,7 +776,7 @@ static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
 }
 
 // skinny_m1w_kernel: one-token products that need whole sums (the SwiGLU epilogue, plain products asked for whole
-// rows; argmax too, not dispatched) of int4 with bf16 scales, symmetric or with zero points, no adapter, on the lean
+// rows, the argmax epilogue) of int4 with bf16 scales, symmetric or with zero points, no adapter, on the lean
 // terms of skinny_m1_kernel: a workgroup takes one pair of tiles over all of K, one wave per 4-group chunk (WK = G / 4
 // waves when that is at most 16; else each wave takes every WK-th chunk, WK = ceil(chunks / ceil(chunks / 16))), each
 // chunk as short-lived as a plain product's wave; the waves' sums meet in LDS and the first wave adds them in wave
@@ -795,8 +788,7 @@ struct M1wArgs {
     const __bf16* x;
     void* y;                // SwiGLU: bf16 [rows / 2]; argmax: f32 logits [rows]
     unsigned long long* keys;
-    unsigned long long* table;  // the argmax spread table and its workgroup counter (argmax_finish)
-    unsigned* count;
+    unsigned long long* table;  // the argmax spread table (argmax_fold_kernel after the launch)
     int tiles, G, valid;
     uint32_t mask, magic;
 };
@@ -887,7 +879,6 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
             if (lane == 0 && k) argmax_spread_max(a.table, 0, k);
         }
     }
-    if (EPI == EPI_ARGMAX) argmax_finish(a.table, a.count, a.keys, 1, threadIdx.x, blockDim.x);
 }
 
 // skinny_mt_kernel: the plain product of 2-5 tokens (up to 8 fit the slots) on the same terms as skinny_m1_kernel (int4 with bf16 scales,
@@ -1650,7 +1641,6 @@ __global__ __launch_bounds__(WM * WN * 64, MINB) void prefill_kernel(Launch a) {
     };
     if (PP && (wave >> 2) != 0) work(std::integral_constant<int, 1>{});
     else work(std::integral_constant<int, 0>{});
-    if (EPI == EPI_ARGMAX) argmax_finish(a, threadIdx.x, blockDim.x);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1668,6 +1658,10 @@ static hipError_t skinny_ng(const Launch& l) {
     if (l.split != 1 && l.split != k.nc) return hipErrorInvalidConfiguration;  // the kernel's two cases
     hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.tile_waves, wk),
                        skinny_lds(l), l.stream, k);
+    if (EPI == EPI_ARGMAX) {
+        const hipError_t e = hipGetLastError();
+        return e != hipSuccess ? e : argmax_fold(l, l.m);
+    }
     return hipGetLastError();
 }
 
@@ -1693,19 +1687,24 @@ static int mw_waves(int nc, int wgs, int cus) {
 // token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
-    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_SILU) {
-        // one token, SwiGLU: the lean workgroup-per-tile-pair kernel when K has at most 16 chunks of 4 groups.
-        // Same-box graph replays, the 27B [gate; up] product (2 x 17408 rows, K 5120): 20.6 -> 18.9 us. The argmax
-        // epilogue stays on skinny_kernel: on the 27B head the twice as many workgroups, each counting itself done
-        // with a returning atomic, made it 20% slower (106 -> 128 us).
+    if constexpr ((F == F_I4 || F == F_ZP) && (EPI == EPI_SILU || EPI == EPI_ARGMAX)) {
+        // one token, SwiGLU or argmax: the lean workgroup-per-tile-pair kernel when K has at most 16 chunks of 4
+        // groups. Same-box graph replays, the 27B [gate; up] product (2 x 17408 rows, K 5120): 20.6 -> 18.9 us; the
+        // 27B head with its argmax (once the fold became a launch of its own: while each workgroup counted itself
+        // done with a returning atomic, twice the workgroups made it 20% slower): the headline step 0.2509 ->
+        // 0.2497 ms.
         const int G = l.cols / QG;
         if (l.m == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && G / 4 <= 16) {
             const int tiles = l.rows / TILE, wk = mw_waves(G / 4, (tiles + 1) / 2, l.cus);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
-                            l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
+                            l.keys, l.argmax_table, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
             hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
                                a);
+            if (EPI == EPI_ARGMAX) {
+                const hipError_t e = hipGetLastError();
+                return e != hipSuccess ? e : argmax_fold(l, 1);
+            }
             return hipGetLastError();
         }
     }
@@ -1716,7 +1715,7 @@ static hipError_t skinny_epi(const Launch& l) {
         if (l.m == 1 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && !l.stage_out) {
             const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
-                            l.keys, l.argmax_table, l.argmax_count, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
+                            l.keys, l.argmax_table, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
             hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
                                a);
@@ -1880,6 +1879,10 @@ static hipError_t prefill_cfg(Launch& l) {
         }
     hipLaunchKernelGGL((prefill_kernel<F, EPI, BMB, TN, WM, WN, MINB, false>), dim3(l.dp_items + l.sk_wgs),
                        dim3(WM * WN * 64), 0, l.stream, l);
+    if (EPI == EPI_ARGMAX) {
+        const hipError_t e = hipGetLastError();
+        return e != hipSuccess ? e : argmax_fold(l, l.m);
+    }
     return hipGetLastError();
 }
 
