@@ -141,7 +141,7 @@ int qh_unpack_row_bf16(size_t rows, size_t cols, const void* codes, size_t p, ui
 /* ---- device: context, matrices, products ---------------------------------------------------------------------- */
 
 /* Gemm::load (core.rs:436-481): a context on `device` (makes it current on this thread). It holds the argmax scratch
- * table and counter, the prefill's stream-K scratch (128 MiB of partial tiles and 4096 item counters) and 32 MiB
+ * table, the prefill's stream-K scratch (128 MiB of partial tiles and 4096 item counters) and 32 MiB
  * for the f16 activations of the prefill's SwiGLU launches, all returned to zero by every launch that uses them;
  * products on one context must therefore not run concurrently on two streams. */
 int qh_open(int device, qh_ctx** out);
@@ -198,7 +198,7 @@ size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, s
  *   epi QH_EPI_SILU: y bf16 [n][rows / 2];
  *   epi QH_EPI_ARGMAX: logit rows: token t reads x row out_rows[t] (int32 device, NULL: t) for t < n_out; y f32
  *     [n_out][rows]; keys[t] (u64 device, cleared by the caller) = max(keys[t], (ordered(v) << 32) | ~o) over the
- *     valid rows o.
+ *     valid rows o (two launches: the product, then a one-workgroup fold of its per-workgroup maxima into keys).
  * Above 48 tokens x's rows 0 .. max(n, n_out) - 1 must lie within 4 GiB of x (32-bit offsets): QH_EINVAL beyond.
  * Returns the split (>= 1) or < 0. Launches only: no host synchronisation, no allocation (graph-capturable). */
 int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, const int32_t* out_rows,
@@ -231,7 +231,7 @@ int qh_gemm_lora(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size
 
 /* qh_gemm without allocation: no counterpart in the reference. For callers that cannot allocate device memory around
  * a product (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments,
- * checks, launch plans and results as qh_gemm, but the launch scratch (argmax table and counter, stream-K partials
+ * checks, launch plans and results as qh_gemm, but the launch scratch (argmax table, stream-K partials
  * and counters, the f16 activations of prefill SwiGLU launches) lives in a static device array of the library
  * (160 MiB + 48.25 KiB per GPU, held until the process ends, set up by qh_open; every process that loads the library
  * reserves it) instead of the context's allocations; it calls no allocating routine. Products never need more scratch
