@@ -83,6 +83,8 @@ class Step:
         self.launches = []
         self.x = torch.randn(max(m, 1), kmax, device="cuda").to(torch.bfloat16)
         self.keys = torch.zeros(max(m, 64), dtype=torch.int64, device="cuda")
+        # the logit rows of an argmax product, gathered as the engine passes them (Step::out_rows)
+        self.out_rows = torch.arange(max(m, 1), dtype=torch.int32, device="cuda")
         self.ys = {}
 
     def add(self, mat, epi, nbytes, flops):
@@ -102,7 +104,7 @@ class Step:
 
         for mat, epi, y, _, _ in self.launches:
             if epi == Epi.Argmax:
-                self.gemm.run(stream, self.m, mat, self.x, y, epi, n_out=self.m, keys=self.keys)
+                self.gemm.run(stream, self.m, mat, self.x, y, epi, out_rows=self.out_rows, n_out=self.m, keys=self.keys)
             else:
                 self.gemm.run(stream, self.m, mat, self.x, y, epi)
 
@@ -891,7 +893,7 @@ def main():
         def run_whole(stream=None):
             for mat, epi, y, _, _ in wst.launches:
                 if epi == Epi.Argmax:
-                    gemm.run(stream, m, mat, wst.x, y, epi, n_out=m, keys=wst.keys)
+                    gemm.run(stream, m, mat, wst.x, y, epi, out_rows=wst.out_rows, n_out=m, keys=wst.keys)
                     continue
                 if mat.rows not in wys:
                     wys[mat.rows] = torch.empty(m * mat.rows, dtype=torch.float32, device="cuda")
@@ -917,7 +919,7 @@ def main():
 
             for mat, epi, y, _, _ in sst.launches:
                 if epi == Epi.Argmax:
-                    gemm.run(stream, 1, mat, sst.x, y, epi, n_out=1, keys=sst.keys)
+                    gemm.run(stream, 1, mat, sst.x, y, epi, out_rows=sst.out_rows, n_out=1, keys=sst.keys)
                     continue
                 split = gemm.run(stream, 1, mat, sst.x, y, epi)
                 key = mat.rows

@@ -785,12 +785,14 @@ struct M1wArgs {
     const u32x4* codes;
     const uint16_t* scales;
     const uint16_t* zeros;  // ZP only
-    const __bf16* x;
+    const __bf16* x;        // the token's row: x row xrows[0] (xrows null: row 0)
     void* y;                // SwiGLU: bf16 [rows / 2]; argmax: f32 logits [rows]
     unsigned long long* keys;
     unsigned long long* table;  // the argmax spread table (argmax_fold_kernel after the launch)
     int tiles, G, valid;
     uint32_t mask, magic;
+    const int32_t* xrows;  // argmax: the token's activations are x row xrows[0] (null: row 0), rows ldx apart
+    int ldx;
 };
 
 template <int EPI, bool ZP>
@@ -808,10 +810,11 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
     asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
     const uint32_t mask = a.mask;
     const int tl[2] = {tile0, t1};
+    const __bf16* const x0 = a.xrows ? a.x + (size_t)a.xrows[0] * a.ldx : a.x;
     float acc[2] = {0.0f, 0.0f};
     // the wave's chunks of 4 groups: wk, wk + WK, ... (one when K has at most 16 chunks)
     for (int gw = 4 * wk; gw < G; gw += 4 * WK) {
-        __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)gw * QG + 8 * lane),
+        __builtin_amdgcn_global_load_lds((const void*)(x0 + (size_t)gw * QG + 8 * lane),
                                          (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t sraw[2][2], zraw[2];
@@ -1687,17 +1690,23 @@ static int mw_waves(int nc, int wgs, int cus) {
 // token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
-    if constexpr ((F == F_I4 || F == F_ZP) && (EPI == EPI_SILU || EPI == EPI_ARGMAX)) {
-        // one token, SwiGLU or argmax: the lean workgroup-per-tile-pair kernel when K has at most 16 chunks of 4
-        // groups. Same-box graph replays, the 27B [gate; up] product (2 x 17408 rows, K 5120): 20.6 -> 18.9 us; the
-        // 27B head with its argmax (once the fold became a launch of its own: while each workgroup counted itself
-        // done with a returning atomic, twice the workgroups made it 20% slower): the headline step 0.2509 ->
-        // 0.2497 ms.
+    if constexpr (F == F_I4 || F == F_ZP) {
+        // Products that need whole sums of their rows, on the workgroup-per-tile-pair kernels (skinny_m1w_kernel at one
+        // token, skinny_mw_kernel for whole plain rows of 2-8 tokens): the one-token argmax, whole plain products, and
+        // the one-token SwiGLU product when K has at most 16 chunks of 4 groups. Same-box graph replays: the 27B
+        // [gate; up] product (2 x 17408 rows, K 5120) 20.6 -> 18.9 us; the 27B head with its argmax, once the fold
+        // became a launch of its own (while each workgroup counted itself done with a returning atomic, twice the
+        // workgroups made it 20% slower), the headline step 0.2509 -> 0.2497 ms (at 5 tokens the head on
+        // skinny_mw_kernel made the step 0.2852 -> 0.3011 ms: it stays on skinny_kernel); whole plain products below
+        // the split product plus the sum of its partials (see qh_gemm's `whole`).
         const int G = l.cols / QG;
-        if (l.m == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && G / 4 <= 16) {
+        const bool fits = !l.lora_rank && G % 4 == 0 &&
+                          ((EPI == EPI_ARGMAX && l.m == 1) || (EPI == EPI_PLAIN && l.split == 1) ||
+                           (EPI == EPI_SILU && l.m == 1 && G / 4 <= 16 && !l.xrows));
+        if (fits && l.m == 1) {
             const int tiles = l.rows / TILE, wk = mw_waves(G / 4, (tiles + 1) / 2, l.cus);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
-                            l.keys, l.argmax_table, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
+                            l.keys, l.argmax_table, tiles, G, l.valid, l.nib_mask, l.bf16_magic, l.xrows, l.ldx};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
             hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
                                a);
@@ -1707,34 +1716,18 @@ static hipError_t skinny_epi(const Launch& l) {
             }
             return hipGetLastError();
         }
-    }
-    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
-        // one token, whole rows (split 1): the workgroup-per-tile-pair kernel, its waves taking one or more chunks of
-        // 4 groups each (at most 16 waves)
-        const int G = l.cols / QG;
-        if (l.m == 1 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0 && !l.stage_out) {
-            const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
-            const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
-                            l.keys, l.argmax_table, tiles, G, l.valid, l.nib_mask, l.bf16_magic};
-            const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
-            hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
-                               a);
-            return hipGetLastError();
-        }
-    }
-    if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
-        // 2-8 tokens, whole rows: the same partition with the multi-token arithmetic
-        const int G = l.cols / QG;
-        if (l.m >= 2 && l.m <= 8 && l.split == 1 && !l.lora_rank && !l.xrows && G % 4 == 0) {
-            const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
-            const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
-                           (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
-            const size_t lds = (size_t)wk * l.m * mt_xpitch<4>() * 2 + (size_t)wk * l.m * 32 * 4;
-            const dim3 grid((tiles + 1) / 2), block(64 * wk);
-            if (l.m == 2) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 2>), grid, block, lds, l.stream, a);
-            else if (l.m == 3) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 3>), grid, block, lds, l.stream, a);
-            else hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 4>), grid, block, lds, l.stream, a);
-            return hipGetLastError();
+        if constexpr (EPI == EPI_PLAIN) {
+            if (fits && l.m >= 2 && l.m <= 8) {
+                const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
+                const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
+                               (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
+                const size_t lds = (size_t)wk * l.m * mt_xpitch<4>() * 2 + (size_t)wk * l.m * 32 * 4;
+                const dim3 grid((tiles + 1) / 2), block(64 * wk);
+                if (l.m == 2) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 2>), grid, block, lds, l.stream, a);
+                else if (l.m == 3) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 3>), grid, block, lds, l.stream, a);
+                else hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 4>), grid, block, lds, l.stream, a);
+                return hipGetLastError();
+            }
         }
     }
     if constexpr ((F == F_I4 || F == F_ZP) && EPI == EPI_PLAIN) {
