@@ -1165,8 +1165,7 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, lds_pt
     const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
                         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
     const uint32_t d = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(bs), "s"(d)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(bs), "{m0}"(d) : "memory");
 }
 
 // buffer resource word 3 (gfx9: 32-bit data format, no swizzle) and the sc1 cache-policy bit of buffer operations
