@@ -427,7 +427,7 @@ extern "C" size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size
     return len;
 }
 
-// qh_gemm's checks and launch, with the scratch (argmax table and counter, stream-K partials and counters) at `sc`.
+// qh_gemm's checks and launch, with the scratch (argmax table, stream-K partials and counters) at `sc`.
 int qh::gemm_with_scratch(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n,
                           const int32_t* out_rows, size_t n_out, void* y, int epi, uint64_t* keys, int whole,
                           const Scratch& sc, const qh_lora* lora) {
