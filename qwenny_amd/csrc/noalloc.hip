@@ -2,7 +2,7 @@
 // array instead of the context's allocations, for callers that cannot allocate device memory around a product (code
 // under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
 //
-// The array holds, in this order, the argmax table and its workgroup counter (ARGMAX_SCRATCH_BYTES), the prefill's
+// The array holds, in this order, the argmax table (ARGMAX_SCRATCH_BYTES), the prefill's
 // stream-K partials and item counters (PF_SK_SCRATCH_BYTES) and the f16 activations of prefill launches with f16
 // operands (X16_SCRATCH_BYTES): the same scratch qh_open allocates per context, so both
 // entry points make the same launch plans and the same results. Every GPU the library runs on holds its own copy
