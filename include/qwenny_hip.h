@@ -198,7 +198,8 @@ size_t qh_part_len(const qh_ctx* ctx, const qh_mat* const* mats, size_t count, s
  *   epi QH_EPI_SILU: y bf16 [n][rows / 2];
  *   epi QH_EPI_ARGMAX: logit rows: token t reads x row out_rows[t] (int32 device, NULL: t) for t < n_out; y f32
  *     [n_out][rows]; keys[t] (u64 device, cleared by the caller) = max(keys[t], (ordered(v) << 32) | ~o) over the
- *     valid rows o (two launches: the product, then a one-workgroup fold of its per-workgroup maxima into keys).
+ *     valid rows o (one launch for one int4 token row, n_out = 1, without an adapter; otherwise two: the product,
+ *     then a one-workgroup fold of its per-workgroup maxima into keys).
  * Above 48 tokens x's rows 0 .. max(n, n_out) - 1 must lie within 4 GiB of x (32-bit offsets): QH_EINVAL beyond.
  * Returns the split (>= 1) or < 0. Launches only: no host synchronisation, no allocation (graph-capturable). */
 int qh_gemm(qh_ctx* ctx, void* stream, const qh_mat* w, const void* x, size_t ldx, size_t n, const int32_t* out_rows,

@@ -135,7 +135,10 @@ __device__ __forceinline__ unsigned long long group16_max(unsigned long long k) 
 // (one atomicMax per token), zeroing it as it reads: the next launch (or graph replay) starts from a clean table. One
 // product at a time per context uses the table (launches on one stream). Against a last-workgroup protocol in the
 // product itself (each workgroup's table updates returned, then a returning count on one counter), the extra launch
-// measured faster: the 27B head 3.8 us per step less.
+// measured faster: the 27B head 3.8 us per step less. The one-token argmax on skinny_m1w_kernel needs neither: each
+// workgroup reads keys[0] once at its start (a lower bound of the final key, as keys only grow) and sends its maximum
+// straight to keys[0] only when above it, so after the first round of workgroups few atomics reach the line (the 27B
+// headline step 0.2517 -> 0.2495 ms against the table and the fold launch).
 __device__ __forceinline__ void argmax_spread_max(unsigned long long* table, int tok, unsigned long long k) {
     const int row = (blockIdx.y * gridDim.x + blockIdx.x) % ARGMAX_SPREAD;
     (void)__hip_atomic_fetch_max(table + row * ARGMAX_MAX_TOK + tok, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -787,8 +790,7 @@ struct M1wArgs {
     const uint16_t* zeros;  // ZP only
     const __bf16* x;        // the token's row: x row xrows[0] (xrows null: row 0)
     void* y;                // SwiGLU: bf16 [rows / 2]; argmax: f32 logits [rows]
-    unsigned long long* keys;
-    unsigned long long* table;  // the argmax spread table (argmax_fold_kernel after the launch)
+    unsigned long long* keys;  // argmax: the token's running key, keys[0]
     int tiles, G, valid;
     uint32_t mask, magic;
     const int32_t* xrows;  // argmax: the token's activations are x row xrows[0] (null: row 0), rows ldx apart
@@ -812,6 +814,10 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
     const int tl[2] = {tile0, t1};
     const __bf16* const x0 = a.xrows ? a.x + (size_t)a.xrows[0] * a.ldx : a.x;
     float acc[2] = {0.0f, 0.0f};
+    // argmax: a lower bound of the token's final key (keys only grow during the launch), read at the coherence point
+    // while the chunks load; the workgroup's maximum is sent only when above it
+    unsigned long long seen = 0;
+    if (EPI == EPI_ARGMAX && wk == 0) seen = __hip_atomic_load(a.keys, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // the wave's chunks of 4 groups: wk, wk + WK, ... (one when K has at most 16 chunks)
     for (int gw = 4 * wk; gw < G; gw += 4 * WK) {
         __builtin_amdgcn_global_load_lds((const void*)(x0 + (size_t)gw * QG + 8 * lane),
@@ -879,7 +885,8 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
             }
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) k = max_u64(k, __shfl_xor(k, o));
-            if (lane == 0 && k) argmax_spread_max(a.table, 0, k);
+            if (lane == 0 && k > seen)
+                (void)__hip_atomic_fetch_max(a.keys, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -1695,7 +1702,8 @@ static hipError_t skinny_epi(const Launch& l) {
         // the one-token SwiGLU product when K has at most 16 chunks of 4 groups. Same-box graph replays: the 27B
         // [gate; up] product (2 x 17408 rows, K 5120) 20.6 -> 18.9 us; the 27B head with its argmax, once the fold
         // became a launch of its own (while each workgroup counted itself done with a returning atomic, twice the
-        // workgroups made it 20% slower), the headline step 0.2509 -> 0.2497 ms (at 5 tokens the head on
+        // workgroups made it 20% slower), the headline step 0.2509 -> 0.2497 ms, and with keys[0] as the workgroups'
+        // filter and target (no fold launch) 0.2495 ms against 0.2517 on another box (at 5 tokens the head on
         // skinny_mw_kernel made the step 0.2852 -> 0.3011 ms: it stays on skinny_kernel); whole plain products below
         // the split product plus the sum of its partials (see qh_gemm's `whole`).
         const int G = l.cols / QG;
@@ -1705,14 +1713,10 @@ static hipError_t skinny_epi(const Launch& l) {
         if (fits && l.m == 1) {
             const int tiles = l.rows / TILE, wk = mw_waves(G / 4, (tiles + 1) / 2, l.cus);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
-                            l.keys, l.argmax_table, tiles, G, l.valid, l.nib_mask, l.bf16_magic, l.xrows, l.ldx};
+                            l.keys, tiles, G, l.valid, l.nib_mask, l.bf16_magic, l.xrows, l.ldx};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
             hipLaunchKernelGGL((skinny_m1w_kernel<EPI, F == F_ZP>), dim3((tiles + 1) / 2), dim3(64 * wk), lds, l.stream,
                                a);
-            if (EPI == EPI_ARGMAX) {
-                const hipError_t e = hipGetLastError();
-                return e != hipSuccess ? e : argmax_fold(l, 1);
-            }
             return hipGetLastError();
         }
         if constexpr (EPI == EPI_PLAIN) {

@@ -188,6 +188,37 @@ def test_argmax_many_workgroups_repeated(gemm, n_out):
         assert rel_err(got, oracle_y(q, x)) <= TOL
 
 
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8g"])
+def test_argmax_running_key(gemm, kind):
+    """keys[] is a running maximum (the caller clears it; products of one step may add to it): a launch leaves
+    max(keys[t], its own best key). One token over 65,536 rows (thousands of workgroups), the caller's key set just
+    below, just above, and far below the launch's best."""
+    import torch
+
+    print(f"argmax running key {kind}", flush=True)
+    n, k = 65536, 512
+    q = make_quant(47, kind, n, k)
+    mat = Mat.stack(gemm, [q])
+    x = to_dev(activations(71, "x", 1, k))
+    y = torch.zeros((1, n), dtype=torch.float32, device="cuda")
+
+    def run(init):
+        keys = torch.tensor([np.int64(np.uint64(init).view(np.int64))], dtype=torch.int64, device="cuda")
+        gemm.run(None, 1, mat, x, y, Epi.Argmax, n_out=1, keys=keys)
+        torch.cuda.synchronize()
+        return int(keys.cpu().numpy().view(np.uint64)[0])
+
+    best = run(0)
+    got = y.cpu().numpy()
+    assert best == int(oracle.argmax_keys(got, n)[0])
+    tenth = int(oracle.argmax_keys(np.sort(got, axis=1)[:, :-9], n - 9)[0])  # a key of a lower logit
+    assert tenth < best
+    assert run(best - 1) == best
+    assert run(best + 1) == best + 1
+    assert run(tenth) == best
+    assert run(0) == best
+
+
 def test_kernel_switch_large_int4(gemm):
     """Split-K plain and SwiGLU products of 33-48 tokens on int4 and grouped int8 matrices of at least 2^26 weights run
     on the prefill kernel (faster there); 32 tokens, whole products, the argmax, per-channel int8 and a matrix one
