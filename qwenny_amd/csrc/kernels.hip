@@ -147,7 +147,7 @@ __device__ __forceinline__ void argmax_spread_max(const Launch& a, int tok, unsi
     argmax_spread_max(a.argmax_table, tok, k);
 }
 
-static __global__ __launch_bounds__(256) void argmax_fold_kernel(unsigned long long* table, unsigned long long* keys,
+static __global__ __launch_bounds__(1024) void argmax_fold_kernel(unsigned long long* table, unsigned long long* keys,
                                                                  int m) {
     __shared__ unsigned long long best[ARGMAX_MAX_TOK];
     for (int t = threadIdx.x; t < m; t += blockDim.x) best[t] = 0;
@@ -166,7 +166,9 @@ static __global__ __launch_bounds__(256) void argmax_fold_kernel(unsigned long l
 
 // the fold after an argmax product's launch (m logit rows)
 static hipError_t argmax_fold(const Launch& l, int m) {
-    hipLaunchKernelGGL(argmax_fold_kernel, dim3(1), dim3(256), 0, l.stream, l.argmax_table, l.keys, m);
+    // a thread per table entry up to 1024 (m <= 16: one exchange round trip per thread)
+    const int threads = std::min(1024, (ARGMAX_SPREAD * m + 63) / 64 * 64);
+    hipLaunchKernelGGL(argmax_fold_kernel, dim3(1), dim3(threads), 0, l.stream, l.argmax_table, l.keys, m);
     return hipGetLastError();
 }
 
