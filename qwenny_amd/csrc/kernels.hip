@@ -702,9 +702,14 @@ struct M1Args {
 };
 
 // workgroups of 4 waves side by side over tiles (2 tiles each), the grid over tile columns x NG-group chunks of K
-// (NG = 4, or 1 when 4-group waves would not fill the chip; skinny_partition)
+// (NG = 4, or 1 when 4-group waves would not fill the chip; skinny_partition).
+// At least two waves per SIMD (amdgpu_waves_per_eu(2)) caps the kernel at 256 registers, which lets the compiler keep
+// the MFMA accumulators in ordinary VGPRs: without it the compiler gave them 48 accumulation registers beside 62 VGPRs,
+// 4 waves per SIMD; with it 68 VGPRs, 7 waves per SIMD (74 and 6 with zero points), so that the whole grid of a 27B
+// product is resident at once. Same box, three A/B pairs: the 27B set 7.43 -> 7.32 us per launch, configs[0] 4.49 ->
+// 4.35 us. (Eight waves per SIMD, 64 VGPRs, spills 16-56 bytes per lane.)
 template <bool ZP, int NG>
-static __global__ __launch_bounds__(256) void skinny_m1_kernel(M1Args a) {
+static __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void skinny_m1_kernel(M1Args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63, wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, kq = lane >> 4;
