@@ -819,7 +819,10 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
     asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.magic));
     const uint32_t mask = a.mask;
     const int tl[2] = {tile0, t1};
-    const __bf16* const x0 = a.xrows ? a.x + (size_t)a.xrows[0] * a.ldx : a.x;
+    // the token's row index through the scalar cache (a uniform load: a vector load here made every wave wait for it
+    // before issuing anything else)
+    const int32_t xrow = a.xrows ? *(const __attribute__((address_space(4))) int32_t*)a.xrows : 0;
+    const __bf16* const x0 = a.x + (size_t)xrow * a.ldx;
     float acc[2] = {0.0f, 0.0f};
     // argmax: a lower bound of the token's final key (keys only grow during the launch), read at the coherence point
     // while the chunks load; the workgroup's maximum is sent only when above it
