@@ -33,6 +33,8 @@ struct qh_ctx {
     int stream_k;
     int skinny_plain_wk;    // skinny kernel, plain products: wave rows over K per workgroup (1; QH_SKINNY_PLAIN_WK)
     int pf_from;            // products from this many tokens take the prefill kernel (QH_PF_FROM, tuning; 49: off)
+    int skinny_few;         // plain products with fewer 4-group waves than this many per CU take 1-group waves (0: by
+                            // token count; QH_SKINNY_FEW, tuning)
 };
 
 int qh::ctx_device(const qh_ctx* ctx) { return ctx->device; }
@@ -104,7 +106,8 @@ extern "C" int qh_open(int device, qh_ctx** out) {
                       std::min(16, std::max(0, env_int("QH_SKINNY_TILE_WAVES", 0))),
                       std::min(9, std::max(0, env_int("QH_PF_SHAPE", 0))), sk, std::max(0, env_int("QH_PF_SK", 1)),
                       std::min(4, std::max(1, env_int("QH_SKINNY_PLAIN_WK", 1))),
-                      std::max(1, env_int("QH_PF_FROM", SKINNY_MAX_M + 1))};
+                      std::max(1, env_int("QH_PF_FROM", SKINNY_MAX_M + 1)),
+                      std::min(64, std::max(0, env_int("QH_SKINNY_FEW", 0)))};
     return QH_OK;
 }
 
@@ -292,8 +295,11 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
     const int cols = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;  // wave columns over the tiles
     // groups per wave: 4 (int4 and int8: 4 KiB or 8 KiB of a tile per wave), 1 for bf16 (4 KiB per group)
     // (plain products whose 4-group waves would number fewer than the chip's SIMDs take one group per wave instead:
-    // 4x the waves in flight; measured +5% at M = 1 and +10% at M = 8 on the 4B layer set, the 27B set unchanged)
-    const bool few = plain && (long)cols * (G / 4) < 4l * ctx->cus;
+    // 4x the waves in flight; measured +5% at M = 1 and +10% at M = 8 on the 4B layer set, the 27B set unchanged;
+    // at 1-2 tokens up to 6 waves per CU: configs[0] (2560, 9728) 4.33 -> 4.10 us, the 4B set at M = 2 3.94 -> 3.90
+    // us, the 27B set the same, while at 5 tokens the 4B set lost 10% and 8 per CU cost the 27B set 1% at 1 token)
+    const int few_per_cu = ctx->skinny_few > 0 ? ctx->skinny_few : (tokens <= 2 ? 6 : 4);
+    const bool few = plain && (long)cols * (G / 4) < (long)few_per_cu * ctx->cus;
     const int ng = !is_bf16(m->wt) && G % 4 == 0 && !few ? 4 : 1;
     const int want_wt = ctx->skinny_tile_waves > 0 ? ctx->skinny_tile_waves : (tokens <= 2 ? 4 : 8);
     if (plain) {
