@@ -903,10 +903,14 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
 
 // skinny_mt_kernel: the plain product of 2-5 tokens (up to 8 fit the slots) on the same terms as skinny_m1_kernel (int4 with bf16 scales,
 // symmetric or with zero points, no adapter): the partition of skinny_kernel's plain products (WT wave columns of 2
-// tiles per workgroup, one chunk of NG groups of K per wave, split = the chunks) and its arithmetic (one MFMA row
-// block of 16 tokens, token 4 (lane / 16) + r in row r of a lane's accumulators), bit for bit. Each wave stages its
-// own tokens' activations (M rows of NG groups, rows 16 bytes apart, global -> LDS directly), so no workgroup barrier
-// separates its loads from its compute, and writes its partials through its LDS slot as 16-byte row runs.
+// tiles per workgroup, one chunk of NG groups of K per wave, split = the chunks) and its arithmetic per token (one
+// MFMA row block of 16 rows), bit for bit. Token t sits in MFMA row 4 (t % 4) + t / 4, so that a lane's accumulator
+// row r holds token 4 r + lane / 16: 2-4 tokens need one accumulator row per lane and 5-8 two (against 2-4 with
+// tokens in row order), which holds the kernel at 74-78 VGPRs, 6 waves per SIMD (5 before). Same-box A/B, three
+// pairs: the 27B step at M = 5 0.2822 -> 0.2788 ms, the 4B set with zero points at M = 4 / 5 4.59 / 4.67 -> 4.23 /
+// 4.41 us per launch, at M = 2 3.91 -> 3.89 us. Each wave stages its own tokens' activations (M rows of NG groups,
+// rows 16 bytes apart, global -> LDS directly), so no workgroup barrier separates its loads from its compute, and
+// writes its partials through its LDS slot as 16-byte row runs.
 struct MtArgs {
     const u32x4* codes;
     const uint16_t* scales;
@@ -971,7 +975,8 @@ static __global__ __launch_bounds__(512) void skinny_mt_kernel(MtArgs a) {
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int r = 0; r < NR; r++) acc[t][r] = 0.0f;
-    const __bf16* xrow0 = xw + min(l16, M - 1) * XP + 8 * kq;  // rows past M read row M - 1 (never stored)
+    // MFMA row l16 holds token 4 (l16 % 4) + l16 / 4; rows past M read row M - 1 (never stored)
+    const __bf16* xrow0 = xw + min(((l16 & 3) << 2) | (l16 >> 2), M - 1) * XP + 8 * kq;
 #pragma unroll
     for (int gi = 0; gi < NG; gi++) {
         u32x4 xa[4];
@@ -1007,7 +1012,7 @@ static __global__ __launch_bounds__(512) void skinny_mt_kernel(MtArgs a) {
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            const int tok = 4 * kq + r;
+            const int tok = 4 * r + kq;
             if (tok < M) stg[tok * 32 + t * TILE + l16] = acc[t][r];
         }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes before its reads
@@ -1023,9 +1028,10 @@ static __global__ __launch_bounds__(512) void skinny_mt_kernel(MtArgs a) {
 // ---------------------------------------------------------------------------------------------------------------
 // skinny_mw_kernel: whole rows (split 1) of a plain product of 2-8 tokens, int4 with bf16 scales, symmetric or with
 // zero points, no adapter: skinny_m1w_kernel's partition (a workgroup per tile pair over all of K, each wave taking
-// every WK-th chunk of 4 groups) with skinny_mt_kernel's arithmetic (each wave stages its tokens' rows of its chunk,
-// 16 bytes apart; token 4 (lane / 16) + r in row r of a lane's accumulators). The waves' sums meet in LDS and the
-// first wave adds them in wave order.
+// every WK-th chunk of 4 groups) with skinny_mt_kernel's arithmetic and token rows (each wave stages its tokens' rows
+// of its chunk, 16 bytes apart; token 4 r + lane / 16 in row r of a lane's accumulators). The waves' sums meet in LDS
+// and the first wave adds them in wave order (the 27B step at M = 5 with whole rows 0.3268 -> 0.3243 ms with the
+// token rows above).
 template <bool ZP, int NR>
 static __global__ __launch_bounds__(1024) void skinny_mw_kernel(MtArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1047,7 +1053,8 @@ static __global__ __launch_bounds__(1024) void skinny_mw_kernel(MtArgs a) {
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int r = 0; r < NR; r++) acc[t][r] = 0.0f;
-    const __bf16* xrow0 = xw + min(l16, M - 1) * XP + 8 * kq;  // rows past M read row M - 1 (never stored)
+    // MFMA row l16 holds token 4 (l16 % 4) + l16 / 4; rows past M read row M - 1 (never stored)
+    const __bf16* xrow0 = xw + min(((l16 & 3) << 2) | (l16 >> 2), M - 1) * XP + 8 * kq;
     for (int gw = 4 * wk; gw < G; gw += 4 * WK) {
         for (int r = 0; r < M; r++)
             __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)r * a.ldx + (size_t)gw * QG + 8 * lane),
@@ -1096,7 +1103,7 @@ static __global__ __launch_bounds__(1024) void skinny_mw_kernel(MtArgs a) {
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            const int tok = 4 * kq + r;
+            const int tok = 4 * r + kq;
             if (tok < M) red[(wk * M + tok) * 32 + t * TILE + l16] = acc[t][r];
         }
     __syncthreads();
@@ -1736,9 +1743,9 @@ static hipError_t skinny_epi(const Launch& l) {
                                (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
                 const size_t lds = (size_t)wk * l.m * mt_xpitch<4>() * 2 + (size_t)wk * l.m * 32 * 4;
                 const dim3 grid((tiles + 1) / 2), block(64 * wk);
-                if (l.m == 2) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 2>), grid, block, lds, l.stream, a);
-                else if (l.m == 3) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 3>), grid, block, lds, l.stream, a);
-                else hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 4>), grid, block, lds, l.stream, a);
+                // accumulator rows per lane: ceil(m / 4)
+                if (l.m <= 4) hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 1>), grid, block, lds, l.stream, a);
+                else hipLaunchKernelGGL((skinny_mw_kernel<F == F_ZP, 2>), grid, block, lds, l.stream, a);
                 return hipGetLastError();
             }
         }
@@ -1779,14 +1786,14 @@ static hipError_t skinny_epi(const Launch& l) {
             };
             using I1 = std::integral_constant<int, 1>;
             using I4 = std::integral_constant<int, 4>;
+            using I2 = std::integral_constant<int, 2>;
+            // accumulator rows per lane: ceil(m / 4)
             if (ng == 4) {
-                if (l.m == 2) go(I4{}, std::integral_constant<int, 2>{});
-                else if (l.m == 3) go(I4{}, std::integral_constant<int, 3>{});
-                else go(I4{}, I4{});
+                if (l.m <= 4) go(I4{}, I1{});
+                else go(I4{}, I2{});
             } else {
-                if (l.m == 2) go(I1{}, std::integral_constant<int, 2>{});
-                else if (l.m == 3) go(I1{}, std::integral_constant<int, 3>{});
-                else go(I1{}, I4{});
+                if (l.m <= 4) go(I1{}, I1{});
+                else go(I1{}, I2{});
             }
             return hipGetLastError();
         }
