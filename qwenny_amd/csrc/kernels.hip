@@ -901,7 +901,7 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
     }
 }
 
-// skinny_mt_kernel: the plain product of 2-5 tokens (up to 8 fit the slots) on the same terms as skinny_m1_kernel (int4 with bf16 scales,
+// skinny_mt_kernel: the plain product of 2-8 tokens on the same terms as skinny_m1_kernel (int4 with bf16 scales,
 // symmetric or with zero points, no adapter): the partition of skinny_kernel's plain products (WT wave columns of 2
 // tiles per workgroup, one chunk of NG groups of K per wave, split = the chunks) and its arithmetic per token (one
 // MFMA row block of 16 rows), bit for bit. Token t sits in MFMA row 4 (t % 4) + t / 4, so that a lane's accumulator
@@ -1767,12 +1767,13 @@ static hipError_t skinny_epi(const Launch& l) {
                 hipLaunchKernelGGL((skinny_m1_kernel<F == F_ZP, 1>), grid, dim3(256), 4 * 4 * QG * 2, l.stream, a);
             return hipGetLastError();
         }
-        // the lean kernel for 2-5 tokens, on the same partition. Same-box graph replays: the 27B step at M = 5
+        // the lean kernel for 2-8 tokens, on the same partition. Same-box graph replays: the 27B step at M = 5
         // 0.302 -> 0.282 ms, the 4B set with zero points at M = 2 4.28 -> 3.95 us per launch, at M = 4 and 5 level;
-        // at M = 8 it lost 3% (its per-wave staging grows the workgroup's LDS with the token count), so from 6 tokens
-        // skinny_kernel's shared staging
+        // at 6-8 tokens it lost 3% to skinny_kernel's shared staging until its token rows (two accumulator rows per
+        // lane from 5 tokens): then the 27B set (no head) at M = 6 / 8 3.68 / 3.69 -> 4.07 / 3.90 TB/s, the 4B set
+        // with zero points at M = 8 4.74 -> 4.69 us per launch
         const int wt = l.tile_waves;
-        if (l.m >= 2 && l.m <= 5 && !l.lora_rank && !l.xrows && (ng == 4 || ng == 1) && l.waves == wt &&
+        if (l.m >= 2 && l.m <= 8 && !l.lora_rank && !l.xrows && (ng == 4 || ng == 1) && l.waves == wt &&
             wt <= 8 && l.split == G / ng && ((uintptr_t)l.y & 15) == 0) {
             const int tiles = l.rows / TILE;
             const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
