@@ -3,7 +3,8 @@
 //
 // Both kernels compute D = X . W^T with the activations as the MFMA A operand and the weights as the B operand, so the
 // packed tile block is the B operand as loaded. The skinny kernel runs v_mfma_f32_16x16x32_bf16 (A 16 tokens x 32 k,
-// B 32 k x 16 outputs; lane l of a wave holds D[token 4 (l / 16) + r][output l % 16], r = 0..3), the prefill kernel
+// B 32 k x 16 outputs; lane l of a wave holds D[row 4 (l / 16) + r][output l % 16], r = 0..3, MFMA row 4 (t % 4) +
+// t / 4 holding token t from two tokens, so that row r of lane l is token 4 r + l / 16), the prefill kernel
 // v_mfma_f32_32x32x16_bf16 (its layout below).
 //
 // skinny_kernel (m <= 48, decode, MTP verify and small batches; from 33 tokens not the plain and SwiGLU products of
@@ -250,7 +251,7 @@ __device__ void lora_delta16(const Launch& a, int tile, int tok0, f32x4& d) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
     const int o = tile * TILE + l16, mod = lora_module_of<SILU>(a, o);
     const int mlo = lora_module_of<SILU>(a, tile * TILE), mhi = lora_module_of<SILU>(a, tile * TILE + TILE - 1);
-    const int tok = min(tok0 + l16, a.m - 1);
+    const int tok = min(tok0 + (((l16 & 3) << 2) | (l16 >> 2)), a.m - 1);  // skinny_kernel's token rows
     const float s = lora_scale_of(a, tok);
     for (int m = mlo; m <= mhi; m++) {
         const int c0 = lora_off(a, m);
@@ -405,11 +406,12 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
     int tt[T];
 #pragma unroll
     for (int t = 0; t < T; t++) tt[t] = min(tile0 + t, tiles - 1);
-    // token block b (16 tokens): lanes read activation row 16 b + l16 (rows past M read row M - 1: their results are
-    // never stored)
+    // token block b (16 tokens): MFMA row l16 holds token 16 b + 4 (l16 % 4) + l16 / 4, so that a lane's accumulator
+    // row r holds token 16 b + 4 r + lane / 16 and NR = ceil(tokens / 4) rows per lane suffice in a partial block (one
+    // token: row order); rows past M read row M - 1 (their results are never stored)
     int xtok[TB];
 #pragma unroll
-    for (int b = 0; b < TB; b++) xtok[b] = min(16 * b + l16, M - 1);
+    for (int b = 0; b < TB; b++) xtok[b] = min(16 * b + (NR > 1 ? (((l16 & 3) << 2) | (l16 >> 2)) : l16), M - 1);
 
     const uint32_t magic_s = a.bf16_magic, mask = a.nib_mask;
     uint32_t magic;  // in a VGPR (copied once; only VALU reads it) so that each pair is one v_and_or_b32
@@ -637,7 +639,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
                 for (int b = 0; b < TB; b++)
 #pragma unroll
                     for (int r = 0; r < NR; r++) {
-                        const int tok = 16 * b + 4 * kq + r;
+                        const int tok = 16 * b + (NR > 1 ? 4 * r + kq : 4 * kq + r);
                         if (tok < M) stg[tok * RW + t * TILE + l16] = acc[b][t][r];
                     }
             const int row0 = tile0 * TILE;
@@ -658,7 +660,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
             for (int b = 0; b < TB; b++)
 #pragma unroll
                 for (int r = 0; r < NR; r++) {
-                    const int tok = 16 * b + 4 * kq + r;
+                    const int tok = 16 * b + (NR > 1 ? 4 * r + kq : 4 * kq + r);
                     const float v = acc[b][t][r];
                     if (EPI == EPI_SILU) {
                         const float up = __shfl_xor(v, 8);
@@ -678,7 +680,7 @@ __global__ __launch_bounds__(TB == 1 ? 1024 : 512) __attribute__((amdgpu_waves_p
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 const unsigned long long k = group16_max(key[b][r]);
-                const int tok = 16 * b + 4 * kq + r;
+                const int tok = 16 * b + (NR > 1 ? 4 * r + kq : 4 * kq + r);
                 if (lead && l16 == 0 && tok < M && k) argmax_spread_max(a, tok, k);
             }
     }
@@ -1710,7 +1712,7 @@ static int mw_waves(int nc, int wgs, int cus) {
     return (nc + per - 1) / per;
 }
 
-// token rows per lane (NR, of a 16-token block: tokens 4 (lane / 16) + r) and 16-token blocks (TB) for m tokens
+// token rows per lane (NR, of a 16-token block: tokens 4 r + lane / 16) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
 static hipError_t skinny_epi(const Launch& l) {
     if constexpr (F == F_I4 || F == F_ZP) {
@@ -1801,12 +1803,13 @@ static hipError_t skinny_epi(const Launch& l) {
     }
     if (l.m > 32) return skinny_nr<F, EPI, 4, 3>(l);
     if (l.m > 16) return skinny_nr<F, EPI, 4, 2>(l);
-    switch (l.m) {
-        case 1: return skinny_nr<F, EPI, 1>(l);
-        case 2: return skinny_nr<F, EPI, 2>(l);
-        case 3: return skinny_nr<F, EPI, 3>(l);
-        default: return skinny_nr<F, EPI, 4>(l);
-    }
+    // accumulator rows per lane: ceil(m / 4), at least 2 from 2 tokens (one row is the one-token form); same-box A/B
+    // against rows in token order (2-4 rows from 2 tokens), three pairs: the 27B step at M = 5 0.2813 -> 0.2780 ms
+    // (its head), int8 per channel at M = 5 0.1490 -> 0.1466 ms per step, one token unchanged
+    if (l.m == 1) return skinny_nr<F, EPI, 1>(l);
+    if (l.m <= 8) return skinny_nr<F, EPI, 2>(l);
+    if (l.m <= 12) return skinny_nr<F, EPI, 3>(l);
+    return skinny_nr<F, EPI, 4>(l);
 }
 
 // The launch plan of one prefill shape: whole items or stream-K for the tail, in l.dp_items / sk_*; returns the
