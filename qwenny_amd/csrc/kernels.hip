@@ -789,10 +789,9 @@ static __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
 // skinny_m1w_kernel: one-token products that need whole sums (the SwiGLU epilogue, plain products asked for whole
 // rows, the argmax epilogue) of int4 with bf16 scales, symmetric or with zero points, no adapter, on the lean
-// terms of skinny_m1_kernel: a workgroup takes one pair of tiles over all of K, one wave per 4-group chunk (WK = G / 4
-// waves when that is at most 16; else each wave takes every WK-th chunk, WK = ceil(chunks / ceil(chunks / 16))), each
-// chunk as short-lived as a plain product's wave; the waves' sums meet in LDS and the first wave adds them in wave
-// order. (skinny_kernel runs these with 2 x 2-wave workgroups whose waves each walk G / 8 chunks, one after another.)
+// terms of skinny_m1_kernel: a workgroup takes one pair of tiles over all of K, one wave per 4-group chunk up to 8
+// chunks, beyond that WK = 8 waves each taking every WK-th chunk (mw_waves), each chunk as short-lived as a plain
+// product's wave; the waves' sums meet in LDS and the first wave adds them in wave order. (skinny_kernel runs these with 2 x 2-wave workgroups whose waves each walk G / 8 chunks, one after another.)
 struct M1wArgs {
     const u32x4* codes;
     const uint16_t* scales;
@@ -830,7 +829,7 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
     // while the chunks load; the workgroup's maximum is sent only when above it
     unsigned long long seen = 0;
     if (EPI == EPI_ARGMAX && wk == 0) seen = __hip_atomic_load(a.keys, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the wave's chunks of 4 groups: wk, wk + WK, ... (one when K has at most 16 chunks)
+    // the wave's chunks of 4 groups: wk, wk + WK, ... (one when K has at most 8 chunks)
     for (int gw = 4 * wk; gw < G; gw += 4 * WK) {
         __builtin_amdgcn_global_load_lds((const void*)(x0 + (size_t)gw * QG + 8 * lane),
                                          (__attribute__((address_space(3))) void*)xw, 16, 0, 0);
@@ -1701,16 +1700,16 @@ static hipError_t skinny_nr(const Launch& l) {
         return l.groups_per_wave == 4 ? skinny_ng<F, EPI, NR, 4, TB>(l) : skinny_ng<F, EPI, NR, 1, TB>(l);
 }
 
-// Waves per workgroup of the workgroup-per-tile-pair kernels for nc chunks of K and wgs workgroups: one chunk each
-// when at most 16, else ceil(nc / 16) chunks each; two chunks each when one would not fit the grid in one round of
-// resident workgroups (two 10-wave workgroups per CU at their 80 registers): at 5 tokens, (5120, 17408) 14.5 -> 12.5 us
-// (at one token, and for the one-token SwiGLU, the same within 1%), while on grids of one round the longer waves lost
-// 10-20%.
-static int mw_waves(int nc, int wgs, int cus) {
-    int per = (nc + 15) / 16;
-    if (per == 1 && nc >= 2 && wgs > std::max(1, 24 / nc) * cus) per = 2;
-    return (nc + per - 1) / per;
-}
+// Waves per workgroup of the workgroup-per-tile-pair kernels for nc chunks of K: a wave per 4-group chunk up to 8,
+// beyond that the chunks dealt out in turn. Eight-wave workgroups fill a CU's 24 wave slots (6 waves per SIMD) with
+// three workgroups, where 10- or 5-wave ones leave 4 idle. Same-box graph replays, us per whole-row product, against
+// the earlier rule (a wave per chunk up to 16, two chunks a wave when the grid would not fit one round of resident
+// workgroups: 10 / 5, 12 and 12 waves here): one token (5120, 17408) 10.70 -> 10.09, (17408, 5120) 11.17 -> 10.88,
+// (5120, 6144) 5.40 -> 5.31, (6144, 5120) 5.52 -> 5.42; five tokens 12.31 -> 11.79, 14.04 -> 12.65, 6.32 -> 6.10,
+// 6.70 -> 6.39; the 27B step with every plain product as whole rows 0.2736 -> 0.2638 ms, the decode layer with its
+// consumers 0.1888 -> 0.1853 ms (its [gate; up] SwiGLU and in-projection on these kernels), the head the same. 6, 4
+// or 16 waves were slower.
+static int mw_waves(int nc) { return std::min(nc, 8); }
 
 // token rows per lane (NR, of a 16-token block: tokens 4 r + lane / 16) and 16-token blocks (TB) for m tokens
 template <int F, int EPI>
@@ -1730,7 +1729,7 @@ static hipError_t skinny_epi(const Launch& l) {
                           ((EPI == EPI_ARGMAX && l.m == 1) || (EPI == EPI_PLAIN && l.split == 1) ||
                            (EPI == EPI_SILU && l.m == 1 && G / 4 <= 16 && !l.xrows));
         if (fits && l.m == 1) {
-            const int tiles = l.rows / TILE, wk = mw_waves(G / 4, (tiles + 1) / 2, l.cus);
+            const int tiles = l.rows / TILE, wk = mw_waves(G / 4);
             const M1wArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.y,
                             l.keys, tiles, G, l.valid, l.nib_mask, l.bf16_magic, l.xrows, l.ldx};
             const size_t lds = (size_t)wk * 4 * QG * 2 + (size_t)wk * 32 * 4;
@@ -1740,7 +1739,7 @@ static hipError_t skinny_epi(const Launch& l) {
         }
         if constexpr (EPI == EPI_PLAIN) {
             if (fits && l.m >= 2 && l.m <= 8) {
-                const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc, (tiles + 1) / 2, l.cus);
+                const int tiles = l.rows / TILE, nc = G / 4, wk = mw_waves(nc);
                 const MtArgs a{(const u32x4*)l.codes, (const uint16_t*)l.scales, l.zeros, (const __bf16*)l.x, l.ldx,
                                (float*)l.y, tiles, G, l.m, l.nib_mask, l.bf16_magic};
                 const size_t lds = (size_t)wk * l.m * mt_xpitch<4>() * 2 + (size_t)wk * l.m * 32 * 4;
