@@ -279,20 +279,25 @@ extern "C" int qh_mat_download(const qh_mat* m, void* codes, void* scales, void*
 // (about 12 per CU) to keep HBM busy, at least a few groups per wave so that its pipeline fills; non-plain epilogues
 // need whole sums in one workgroup (split 1).
 struct Partition {
-    int tile_waves, waves, split, groups_per_wave;
+    int tile_waves, waves, split, groups_per_wave, tiles_per_wave;
 };
 
 // The skinny kernel's partition of a product of m tokens (kernels.hip skinny_kernel): each wave takes SKINNY_TILES
-// tiles and 4 groups (1 when the group count is not a multiple of 4); a workgroup stages the activations of its
-// super-chunk of K once for all its waves, so the more wave columns (tile_waves) share it, the less that costs
-// relative to the weights (m / (4 * tile_waves * SKINNY_TILES) of the int4 bytes).
+// tiles (one-token plain int8 and bf16 products: one) and 4 groups (1 when the group count is not a multiple of 4); a
+// workgroup stages the activations of its super-chunk of K once for all its waves, so the more wave columns
+// (tile_waves) share it, the less that costs relative to the weights (m / (4 * tile_waves * SKINNY_TILES) of the int4
+// bytes).
 // Plain products: workgroups of wave columns side by side over tiles, the grid split over every chunk of K (split-K
 // partials the consumer sums). Other epilogues need whole sums in one workgroup: its wave rows split K (reduced
 // through LDS), as few as give the launch enough waves to fill the CUs, dividing the chunks evenly and fitting the wave
 // and LDS limits; longer K is walked in super-chunks.
 static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tokens, bool plain) {
     const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
-    const int cols = (tiles + SKINNY_TILES - 1) / SKINNY_TILES;  // wave columns over the tiles
+    // tiles per wave: one for one-token plain int8 and bf16 products (8 KiB of one tile, half the registers of a
+    // two-tile wave, 5 waves per SIMD for int8: same-box graph replays, int8 per channel 27B set 5.39 -> 5.49 TB/s,
+    // grouped int8 5.49 -> 5.69, dense bf16 6.12 -> 6.17; at 5 tokens two tiles stay ahead, -0.5%)
+    const int tpw = plain && tokens == 1 && (is_i8(m->wt) || is_bf16(m->wt)) ? 1 : SKINNY_TILES;
+    const int cols = (tiles + tpw - 1) / tpw;  // wave columns over the tiles
     // groups per wave: 4 (int4 and int8: 4 KiB or 8 KiB of a tile per wave), 1 for bf16 (4 KiB per group)
     // (plain products whose 4-group waves would number fewer than the chip's SIMDs take one group per wave instead:
     // 4x the waves in flight; measured +5% at M = 1 and +10% at M = 8 on the 4B layer set, the 27B set unchanged;
@@ -307,8 +312,8 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
         // QH_SKINNY_PLAIN_WK (tuning): wave rows over K within the workgroup, dividing the partials
         const int pk = ctx->skinny_plain_wk;
         if (pk > 1 && (G / ng) % pk == 0 && wt * pk <= (tokens > 16 ? 8 : 16))
-            return Partition{wt, wt * pk, G / ng / pk, ng};
-        return Partition{wt, wt, G / ng, ng};
+            return Partition{wt, wt * pk, G / ng / pk, ng, tpw};
+        return Partition{wt, wt, G / ng, ng, tpw};
     }
     const size_t per_group = std::max<size_t>(tokens, 1) * QG * 2;  // LDS bytes of one group's activations
     // above 16 tokens (several 16-token blocks per wave) workgroups of at most 8 waves: the kernel's register budget
@@ -325,7 +330,7 @@ static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tok
         wk = w;
         if (wt * w >= 4 && wgs * wt * w >= (long)ctx->skinny_fill * ctx->cus) break;
     }
-    return Partition{wt, wt * wk, 1, ng};
+    return Partition{wt, wt * wk, 1, ng, tpw};
 }
 
 // Whether the skinny kernel takes a product of m tokens (else the prefill kernel): up to SKINNY_MAX_M tokens, except
@@ -387,12 +392,14 @@ static Launch make_launch(const qh_ctx* ctx, const qh_mat* w, const void* x, siz
         l.waves = p.waves;
         l.split = p.split;
         l.groups_per_wave = p.groups_per_wave;
+        l.tiles_per_wave = p.tiles_per_wave;
         // 16-byte row runs need a 16-byte aligned y (its rows are: the row count is a multiple of 16)
         // (one token: the LDS round trip costs more than it saves, measured 3% on small matrices)
         l.stage_out = epi == QH_EPI_PLAIN && m > 1 && ((uintptr_t)y & 15) == 0;
     } else {
         l.tile_waves = 4;
         l.waves = 4;
+        l.tiles_per_wave = SKINNY_TILES;
         l.split = 1;  // the prefill launcher sets it (K-sliced plain products write several partials)
     }
     return l;

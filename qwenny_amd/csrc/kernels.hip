@@ -1677,14 +1677,22 @@ template <int F, int EPI, int NR, int NG, int TB>
 static hipError_t skinny_ng(const Launch& l) {
     if (64 * l.waves > (TB == 1 ? 1024 : 512)) return hipErrorInvalidConfiguration;  // the kernel's launch bound
     const int tiles = l.rows / TILE;
-    const int per_wg = SKINNY_TILES * l.tile_waves;
+    const int per_wg = l.tiles_per_wave * l.tile_waves;
     dim3 grid((tiles + per_wg - 1) / per_wg, l.split);
     Launch k = l;
     const int wk = l.waves / l.tile_waves;
     k.nc = l.cols / QG / (wk * NG);
     if (l.split != 1 && l.split != k.nc) return hipErrorInvalidConfiguration;  // the kernel's two cases
-    hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.tile_waves, wk),
-                       skinny_lds(l), l.stream, k);
+    // one tile per wave: one-token plain int8 and bf16 products (the partition's choice)
+    constexpr bool T1 = EPI == EPI_PLAIN && NR == 1 && TB == 1 && (F & (F_I8 | F_BF16));
+    if (T1 && l.tiles_per_wave == 1)
+        hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, 1, NG, TB>), grid, dim3(64 * l.tile_waves, wk), skinny_lds(l),
+                           l.stream, k);
+    else if (l.tiles_per_wave == SKINNY_TILES)
+        hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, SKINNY_TILES, NG, TB>), grid, dim3(64 * l.tile_waves, wk),
+                           skinny_lds(l), l.stream, k);
+    else
+        return hipErrorInvalidConfiguration;
     if (EPI == EPI_ARGMAX) {
         const hipError_t e = hipGetLastError();
         return e != hipSuccess ? e : argmax_fold(l, l.m);
@@ -1964,9 +1972,9 @@ size_t skinny_lds(const Launch& l) {
     const size_t x0 = (size_t)l.m * (wk * l.groups_per_wave * QG + 8) * 2;  // the workgroup's staged rows
     const size_t xw = skinny_wave_x(l.m, l.fmt, l.groups_per_wave) ? (size_t)l.waves * l.groups_per_wave * QG * 2 : 0;
     const size_t x = (std::max(x0, xw) + 15) & ~(size_t)15;
-    const size_t red = (size_t)(wk - 1) * l.tile_waves * tb * SKINNY_TILES * 4 * 64 * sizeof(float);
-    // plain partials staged per tile column's lead wave: m tokens x SKINNY_TILES tiles of f32
-    const size_t out = l.stage_out ? (size_t)l.tile_waves * l.m * SKINNY_TILES * TILE * sizeof(float) : 0;
+    const size_t red = (size_t)(wk - 1) * l.tile_waves * tb * l.tiles_per_wave * 4 * 64 * sizeof(float);
+    // plain partials staged per tile column's lead wave: m tokens x tiles_per_wave tiles of f32
+    const size_t out = l.stage_out ? (size_t)l.tile_waves * l.m * l.tiles_per_wave * TILE * sizeof(float) : 0;
     return x + std::max(red, out);
 }
 
