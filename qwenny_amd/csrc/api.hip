@@ -283,7 +283,7 @@ struct Partition {
 };
 
 // The skinny kernel's partition of a product of m tokens (kernels.hip skinny_kernel): each wave takes SKINNY_TILES
-// tiles (one-token plain int8 and bf16 products: one) and 4 groups (1 when the group count is not a multiple of 4); a
+// tiles (plain int8 and bf16 products of 1-2 tokens: one) and 4 groups (1 when the group count is not a multiple of 4); a
 // workgroup stages the activations of its super-chunk of K once for all its waves, so the more wave columns
 // (tile_waves) share it, the less that costs relative to the weights (m / (4 * tile_waves * SKINNY_TILES) of the int4
 // bytes).
@@ -293,10 +293,11 @@ struct Partition {
 // and LDS limits; longer K is walked in super-chunks.
 static Partition skinny_partition(const qh_ctx* ctx, const qh_mat* m, size_t tokens, bool plain) {
     const int tiles = (int)(m->rows / TILE), G = (int)(m->cols / QG);
-    // tiles per wave: one for one-token plain int8 and bf16 products (8 KiB of one tile, half the registers of a
-    // two-tile wave, 5 waves per SIMD for int8: same-box graph replays, int8 per channel 27B set 5.39 -> 5.49 TB/s,
-    // grouped int8 5.49 -> 5.69, dense bf16 6.12 -> 6.17; at 5 tokens two tiles stay ahead, -0.5%)
-    const int tpw = plain && tokens == 1 && (is_i8(m->wt) || is_bf16(m->wt)) ? 1 : SKINNY_TILES;
+    // tiles per wave: one for plain int8 and bf16 products of 1-2 tokens (8 KiB of one tile, half the registers of a
+    // two-tile wave, 5 waves per SIMD for int8: same-box graph replays, int8 per channel 27B set at M = 1 5.39 -> 5.49
+    // TB/s, grouped int8 5.49 -> 5.69, dense bf16 6.12 -> 6.17; at M = 2 int8 5.04 -> 5.19 TB/s, grouped 5.00 ->
+    // 5.17; from 3 tokens two tiles stay level or ahead, -0.5% at 5)
+    const int tpw = plain && tokens <= 2 && (is_i8(m->wt) || is_bf16(m->wt)) ? 1 : SKINNY_TILES;
     const int cols = (tiles + tpw - 1) / tpw;  // wave columns over the tiles
     // groups per wave: 4 (int4 and int8: 4 KiB or 8 KiB of a tile per wave), 1 for bf16 (4 KiB per group)
     // (plain products whose 4-group waves would number fewer than the chip's SIMDs take one group per wave instead:

@@ -36,7 +36,7 @@ struct Launch {
     int waves;              // waves per workgroup (skinny kernel): tile_waves over tiles x waves / tile_waves over K
     int tile_waves;
     int groups_per_wave;    // skinny kernel: 4, or 1 when the group count is not a multiple of 4
-    int tiles_per_wave;     // skinny kernel: SKINNY_TILES, or 1 (one-token plain int8 and bf16 products)
+    int tiles_per_wave;     // skinny kernel: SKINNY_TILES, or 1 (plain int8 and bf16 products of 1-2 tokens)
     int nc;                 // skinny kernel: super-chunks of K (groups / (wave rows x groups_per_wave)); set at launch
     int stage_out;          // skinny kernel, plain products: partials written through LDS in 16-byte row runs
     int cus;                // compute units (the prefill shape choice)

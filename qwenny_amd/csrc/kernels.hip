@@ -1683,8 +1683,8 @@ static hipError_t skinny_ng(const Launch& l) {
     const int wk = l.waves / l.tile_waves;
     k.nc = l.cols / QG / (wk * NG);
     if (l.split != 1 && l.split != k.nc) return hipErrorInvalidConfiguration;  // the kernel's two cases
-    // one tile per wave: one-token plain int8 and bf16 products (the partition's choice)
-    constexpr bool T1 = EPI == EPI_PLAIN && NR == 1 && TB == 1 && (F & (F_I8 | F_BF16));
+    // one tile per wave: plain int8 and bf16 products of 1-2 tokens (the partition's choice)
+    constexpr bool T1 = EPI == EPI_PLAIN && NR <= 2 && TB == 1 && (F & (F_I8 | F_BF16));
     if (T1 && l.tiles_per_wave == 1)
         hipLaunchKernelGGL((skinny_kernel<F, EPI, NR, 1, NG, TB>), grid, dim3(64 * l.tile_waves, wk), skinny_lds(l),
                            l.stream, k);
