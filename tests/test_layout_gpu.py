@@ -169,6 +169,21 @@ def test_part_len(gemm):
     assert mats[1].split(SKINNY_MAX_M) > 4 and 1 <= mats[1].split(SKINNY_MAX_M + 1) <= 16 and mats[1].split(513) == 1
 
 
+def test_split_by_token_count(gemm):
+    """A matrix whose 4-group waves would number too few per CU takes one group per wave (split = groups of K) at 1-2
+    tokens and 4 groups from 3 (split = chunks); part_len covers both. configs[0]'s (2560, 9728): 304 wave columns x 5
+    chunks = 1520 waves, below 6 per CU at one token, not below 4 from 3 tokens."""
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    q = make_quant(79, "i4", 9728, 2560)
+    mat = Mat.stack(gemm, [q])
+    waves = 304 * 5
+    want = [20 if waves < (6 if n <= 2 else 4) * cus else 5 for n in (1, 2, 3, 5)]
+    assert [mat.split(n) for n in (1, 2, 3, 5)] == want
+    assert gemm.part_len([mat], 8) >= max(mat.split(n) * n * mat.rows for n in range(1, 9))
+
+
 def test_checkpoint_end_to_end(gemm, tmp_path):
     """A compressed-tensors checkpoint on disk (gate with zero points, up and down symmetric) through Checkpoint,
     Quant.stack and Mat.stack into the SwiGLU product and the plain product after it."""
