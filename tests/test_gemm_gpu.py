@@ -57,12 +57,13 @@ def test_skinny_plain(gemm, kind, m):
     _check(_plain(gemm, mat, x, m), q, x, mat.kernel(m))
 
 
-@pytest.mark.parametrize("kind", ["i4", "i4z"])
+@pytest.mark.parametrize("kind", ["i4", "i4z", "i8", "i8g"])
 @pytest.mark.parametrize("m", [1, 2, 5])
 @pytest.mark.parametrize("rows,cols", [(16, 512), (48, 512), (80, 1024), (400, 2560)])
 def test_decode_odd_tiles(gemm, kind, m, rows, cols):
     """Decode products of 1, 3, 5 and 25 tiles (the last wave of a pair holding one tile), with 4-group and one-group
-    waves: the lean decode kernels' edges. Each output against the oracle; the returned split matches Mat.split."""
+    waves: the lean decode kernels' edges, and int8's one-tile waves at 1-2 tokens. Each output against the oracle;
+    the returned split matches Mat.split."""
     print(f"decode odd tiles {kind} m={m} {rows}x{cols}", flush=True)
     q = make_quant(60 + rows + m, kind, rows, cols)
     x = activations(61 + m, "x", m, cols)
